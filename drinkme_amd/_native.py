@@ -1,0 +1,80 @@
+"""ctypes binding of libdmx_radix.so (include/dmx_radix.h).
+
+The library is built in-tree by `python -m drinkme_amd.build` (or
+__graft_entry__.build()). There is no fallback: a missing library raises
+here, at first use, with the path it looked for.
+"""
+
+from __future__ import annotations
+
+import ctypes as ct
+import os
+
+from .build import LIB
+
+DMX_BF16 = 0
+DMX_F32 = 1
+POLICY_AUTO = 0
+POLICY_GENERIC = 1
+
+
+class RadixTensor(ct.Structure):
+    """dmx_radix_tensor."""
+    _fields_ = [
+        ("data", ct.c_void_p),
+        ("offsets", ct.c_void_p),
+        ("palette", ct.c_void_p),
+        ("schedule", ct.c_void_p),
+        ("payload_words", ct.c_uint64),
+        ("pad_words", ct.c_uint64),
+        ("rows", ct.c_uint32),
+        ("cols", ct.c_uint32),
+        ("block_size", ct.c_uint32),
+        ("n_widths", ct.c_uint32),
+        ("widths", ct.c_uint32 * 8),
+    ]
+
+
+# every symbol include/dmx_radix.h declares, with its ctypes signature
+_P, _U64, _U32, _I, _SZ = ct.c_void_p, ct.c_uint64, ct.c_uint32, ct.c_int, ct.c_size_t
+_TP = ct.POINTER(RadixTensor)
+SIGNATURES = {
+    "dmx_abi_version": (_I, []),
+    "dmx_radix_pad_words": (_U64, [_U32, _P, _U32]),
+    "dmx_radix_native": (_I, [_U32, _P, _U64, _U64, _U64, _U64, _U32, _U32, _P, _U32, _P, _P, _P, _U64, _U64, _U64,
+                              _P, _P, _U64]),
+    "dmx_set_host_threads": (_I, [_I]),
+    "dmx_radix_decode": (_I, [_TP, _P, _P, _P, _SZ]),
+    "dmx_radix_prepare": (_I, [_TP, _P, _P, _P, _SZ]),
+    "dmx_radix_gemv": (_I, [_TP, _P, _I, _U32, _P, _I, _P, _I, _P, _P, _SZ]),
+    "dmx_radix_set_policy": (_I, [_I]),
+    "dmx_synth_bf16": (_I, [_U64, _U64, _U64, ct.c_double, _U32, _P, _P, _SZ]),
+}
+
+_lib = None
+
+
+def lib():
+    """The loaded library (raises when it is not built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB):
+            raise ImportError(f"libdmx_radix.so is not built ({LIB}); run `python -m drinkme_amd.build`")
+        L = ct.CDLL(LIB)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        if L.dmx_abi_version() != 1:
+            raise ImportError(f"{LIB}: ABI version {L.dmx_abi_version()}, expected 1")
+        _lib = L
+    return _lib
+
+
+def error_buffer():
+    return ct.create_string_buffer(512)
+
+
+def check(status: int, err, what: str) -> None:
+    if status:
+        raise RuntimeError(f"{what}: {err.value.decode(errors='replace')}")

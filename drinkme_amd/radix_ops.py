@@ -1,0 +1,165 @@
+"""drinkme's radix_ops surface (src/drinkme/codec/radix_ops.py:341-441) over
+libdmx_radix.so: the same functions, arguments and results, so the module
+seam that binds radix_ops (src/drinkme/codec/swap.py:60-65) can bind this
+module instead.
+
+  gemv_fused(p, x, bias, out_dtype)  x [C] -> [1, R], bias in fp32, one rounding
+  gemv(p, x)                         x [C] -> fp32 [R], no bias
+  gemv_mc(p, x)                      x [M, C], 1 <= M <= 8 -> fp32 [M, R]
+  gemv_rows(p, x, bias, out_dtype)   x [M, C] -> [M, R], bias and one rounding
+                                     fused (the mc arm plus swap's epilogue)
+  decode_bits(p)                     -> u16 [R, C], the source bit patterns
+  decode_weight(p)                   -> bf16 [R, C]
+  prepare_schedule(...)              -> u16 [nblocks], the gulp stream lengths
+  read_bytes(p)                      bytes one call streams
+
+`p` is a runtime dict from swap.to_device_radix. Every call launches on
+torch's current stream and allocates only its output, with torch.
+"""
+
+from __future__ import annotations
+
+import ctypes as ct
+
+import torch
+
+from . import _native
+
+MC_MAX = 8  # src/drinkme/codec/ops.py:19
+
+_DTYPE = {torch.bfloat16: _native.DMX_BF16, torch.float32: _native.DMX_F32}
+
+
+def _stream():
+    return ct.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def descriptor(p: dict) -> _native.RadixTensor:
+    """The dmx_radix_tensor of a runtime dict (built once, kept in the dict)."""
+    t = p.get("_dmx")
+    if t is None:
+        widths = [int(w) for w in p["widths"]]
+        t = _native.RadixTensor()
+        t.data = p["rx_data"].data_ptr()
+        t.offsets = p["rx_offsets"].data_ptr()
+        t.palette = p["rx_palette"].data_ptr()
+        sched = p.get("rx_schedule")
+        t.schedule = sched.data_ptr() if sched is not None and sched.numel() else None
+        t.payload_words = int(p["NW"])
+        t.pad_words = int(p["rx_pad_words"])
+        t.rows, t.cols, t.block_size = int(p["R"]), int(p["C"]), int(p["block_size"])
+        t.n_widths = len(widths)
+        for i, w in enumerate(widths):
+            t.widths[i] = w
+        p["_dmx"] = t
+    return t
+
+
+def _dtype_code(dtype, what):
+    if dtype not in _DTYPE:
+        raise TypeError(f"{what}: {dtype} is not bf16 or fp32")
+    return _DTYPE[dtype]
+
+
+def gemv_rows(p: dict, x: torch.Tensor, bias=None, out_dtype=torch.float32) -> torch.Tensor:
+    """x [M, C] (bf16 or fp32, 1 <= M <= 8) -> [M, R] in out_dtype: the rows
+    accumulated in fp32, the bias (bf16 or fp32, or None) added in fp32,
+    one rounding."""
+    if x.dim() != 2 or x.shape[1] != int(p["C"]):
+        raise ValueError(f"radix gemv: x must be [M, {p['C']}], got {tuple(x.shape)}")
+    M = x.shape[0]
+    if not 1 <= M <= MC_MAX:
+        raise ValueError(f"radix gemv_mc: M={M} outside 1..{MC_MAX}")
+    if x.device != p["rx_data"].device:
+        raise ValueError("radix gemv: x is not on the weight's device")
+    x = x.contiguous()
+    R = int(p["R"])
+    out = torch.empty((M, R), dtype=out_dtype, device=x.device)
+    xd = _dtype_code(x.dtype, "activation")
+    od = _dtype_code(out_dtype, "output")
+    if bias is not None:
+        bias = bias.contiguous()
+        bd = _dtype_code(bias.dtype, "bias")
+        if bias.numel() != R or bias.device != x.device:
+            raise ValueError("radix gemv: bias must hold R elements on the weight's device")
+    else:
+        bd = 0
+    err = _native.error_buffer()
+    st = _native.lib().dmx_radix_gemv(ct.byref(descriptor(p)), x.data_ptr(), xd, M,
+                                       bias.data_ptr() if bias is not None else None, bd, out.data_ptr(), od,
+                                       _stream(), err, len(err))
+    _native.check(st, err, "dmx_radix_gemv")
+    return out
+
+
+def gemv_fused(p: dict, x: torch.Tensor, bias, out_dtype=torch.bfloat16) -> torch.Tensor:
+    """The M = 1 arm: x [C] -> [1, R] in out_dtype, bias added in fp32
+    before the single rounding (src/drinkme/codec/radix_ops.py:351-370)."""
+    return gemv_rows(p, x.reshape(1, -1), bias, out_dtype)
+
+
+def gemv(p: dict, x: torch.Tensor) -> torch.Tensor:
+    """The M = 1 arm's fp32 [R] result, no bias (radix_ops.py:373-376)."""
+    return gemv_rows(p, x.reshape(1, -1), None, torch.float32).reshape(-1)
+
+
+def gemv_mc(p: dict, x: torch.Tensor) -> torch.Tensor:
+    """x [M, C], 1 <= M <= 8 -> fp32 [M, R] (radix_ops.py:379-398)."""
+    return gemv_rows(p, x, None, torch.float32)
+
+
+def decode_bits(p: dict, num_warps: int | None = None) -> torch.Tensor:
+    """Every block once -> the original u16 bit patterns [R, C]
+    (radix_ops.py:418-427). `num_warps` is accepted for the signature and
+    ignored: the launch shape is the library's."""
+    del num_warps
+    R, C = int(p["R"]), int(p["C"])
+    out = torch.empty((R, C), dtype=torch.uint16, device=p["rx_data"].device)
+    err = _native.error_buffer()
+    st = _native.lib().dmx_radix_decode(ct.byref(descriptor(p)), out.data_ptr(), _stream(), err, len(err))
+    _native.check(st, err, "dmx_radix_decode")
+    return out
+
+
+def decode_weight(p: dict) -> torch.Tensor:
+    """The transient bf16 weight [R, C] for F.linear (radix_ops.py:430-432)."""
+    return decode_bits(p).view(torch.bfloat16)
+
+
+def prepare_schedule(data, offsets, C: int, widths, B: int, nblocks: int) -> torch.Tensor:
+    """The per-block tier stream lengths, 2 bytes per block, on the device
+    (radix_ops.py:341-348). `data` must carry the reach pad."""
+    widths = [int(w) for w in widths]
+    nb = -(-int(C) // int(B))
+    t = _native.RadixTensor()
+    t.data = data.data_ptr()
+    t.offsets = offsets.data_ptr()
+    t.palette = None
+    t.schedule = None
+    pad = int(_native.lib().dmx_radix_pad_words(int(B), (ct.c_uint32 * 8)(*widths), len(widths)))
+    t.payload_words = max(int(data.numel()) - pad, 0)
+    t.pad_words = pad
+    t.rows, t.cols, t.block_size = int(nblocks) // nb, int(C), int(B)
+    t.n_widths = len(widths)
+    for i, w in enumerate(widths):
+        t.widths[i] = w
+    sched = torch.empty(int(nblocks), dtype=torch.uint16, device=data.device)
+    err = _native.error_buffer()
+    st = _native.lib().dmx_radix_prepare(ct.byref(t), sched.data_ptr(), _stream(), err, len(err))
+    _native.check(st, err, "dmx_radix_prepare")
+    return sched
+
+
+def read_bytes(p: dict) -> int:
+    """Bytes one GEMV call streams: the payload (NW words, not the pad),
+    the directory, the tables and the schedule (radix_ops.py:435-441)."""
+    words = int(p["NW"]) if "NW" in p else p["rx_data"].numel()
+    return words * 4 + sum(p[k].numel() * p[k].element_size() for k in ("rx_offsets", "rx_palette", "rx_schedule"))
+
+
+def set_policy(policy: str) -> str:
+    """'auto' (specialised kernels where they apply) or 'generic'; returns
+    the previous one."""
+    code = {"auto": _native.POLICY_AUTO, "generic": _native.POLICY_GENERIC}[policy]
+    prev = _native.lib().dmx_radix_set_policy(code)
+    return {_native.POLICY_AUTO: "auto", _native.POLICY_GENERIC: "generic"}[prev]

@@ -1,0 +1,142 @@
+/*
+ * dmx_radix.h — the C ABI of drinkme_amd's MI355X (gfx950) radix codec
+ * library, libdmx_radix.so.
+ *
+ * It replaces drinkme's fused radix decode + matmul path: the Triton module
+ * codec/radix_ops.py that codec/swap.py binds through its one seam,
+ * _bind_radix_ops (src/drinkme/codec/swap.py:60-65), plus the CPU codec's
+ * single C entry point radix_native (src/drinkme/codec/radix_native.cpp:
+ * 211-236). Every entry point below names the drinkme interface it stands
+ * in for.
+ *
+ * Conventions (those of radix_native.cpp:211-236):
+ *   - every entry point returns int: 0 on success, nonzero on a refusal;
+ *     a refusal writes a NUL-terminated message into `err` (`errn` bytes);
+ *   - every buffer is caller-owned: the library never allocates device
+ *     memory and never frees; a device entry point only launches kernels
+ *     on `stream` (a hipStream_t; NULL is the null stream) and returns
+ *     without synchronising;
+ *   - arguments are checked on the host before any launch, so a refusal
+ *     launches nothing;
+ *   - no per-load bounds in the kernels: `data` must carry at least
+ *     dmx_radix_pad_words(block_size, widths) zero words after the payload
+ *     (the reach pad, src/drinkme/codec/swap.py:84-95, :134-136) and the
+ *     directory must have passed the descriptor gate
+ *     (src/drinkme/codec/radix.py:174-238); then no read leaves the
+ *     allocation, whatever the payload words hold.
+ *
+ * Formats: bf16 weights only; the radix stream layout of
+ * docs/pack-format.md / src/drinkme/codec/radix.py:77-136 unchanged.
+ */
+#ifndef DMX_RADIX_H
+#define DMX_RADIX_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define DMX_ABI_VERSION 1
+
+/* element types of activations, biases and outputs */
+#define DMX_BF16 0
+#define DMX_F32 1
+
+/* dmx_radix_set_policy */
+#define DMX_POLICY_AUTO 0    /* the specialised kernels where they apply */
+#define DMX_POLICY_GENERIC 1 /* the generic decoder for every tensor */
+
+/* One radix tensor resident on the device: the runtime dict of
+ * swap.to_device_radix (src/drinkme/codec/swap.py:80-161) as plain
+ * pointers and scalars. */
+typedef struct dmx_radix_tensor {
+    const uint32_t* data;     /* rx_data: payload_words words, then pad_words zero words */
+    const uint32_t* offsets;  /* rx_offsets: rows * ceil(cols / block_size) + 1 words */
+    const uint32_t* palette;  /* rx_palette: each nonterminal tier's (1 << w) - 1 entries
+                                 zero-padded to whole words, tiers concatenated
+                                 (src/drinkme/codec/radix_pack.py:333-350) */
+    const uint16_t* schedule; /* rx_schedule: one u16 per block for > 2 tiers, else NULL
+                                 (read by no kernel of this library; carried so the
+                                 descriptor is the runtime dict's) */
+    uint64_t payload_words;   /* NW */
+    uint64_t pad_words;       /* zero words after the payload */
+    uint32_t rows;            /* R */
+    uint32_t cols;            /* C */
+    uint32_t block_size;      /* B: power of two 32..4096 (the served format: 1024) */
+    uint32_t n_widths;        /* tier count, terminal included: 2..8 */
+    uint32_t widths[8];       /* tier widths; the last is 8 (the bf16 exponent) */
+} dmx_radix_tensor;
+
+/* DMX_ABI_VERSION of the loaded library. No drinkme counterpart (the
+ * ctypes loader's version probe, src/drinkme/codec/radix_native.py:105-151). */
+int dmx_abi_version(void);
+
+/* The farthest word past a block's start any reader asks for:
+ * block_word_bounds(B)[1] (src/drinkme/codec/radix.py:149-171); sip 608,
+ * gulp 768 at B = 1024. 0 for invalid widths. */
+uint64_t dmx_radix_pad_words(uint32_t block_size, const uint32_t* widths, uint32_t n_widths);
+
+/* Replaces radix_native (src/drinkme/codec/radix_native.cpp:211-236) with
+ * the same signature and meaning: op 0 plan (palette tables + directory,
+ * *result = payload words), 1 encode, 2 decode rows [first, first + nrows)
+ * into the pointer given (row `first` at its start), 3 validate the
+ * palette tables. 1024-weight blocks; palettes per region of rg rows x cg
+ * blocks. Runs on host threads (dmx_set_host_threads). */
+int dmx_radix_native(uint32_t op, void* source_or_output, uint64_t rows, uint64_t cols, uint64_t rg,
+                     uint64_t cg, uint32_t mant, uint32_t exponent, const uint32_t* widths, uint32_t count,
+                     uint8_t* palettes, uint32_t* offsets, uint32_t* data, uint64_t words, uint64_t first,
+                     uint64_t nrows, uint64_t* result, char* error, uint64_t error_size);
+
+/* Host threads for dmx_radix_native and dmx_synth_bf16 (0 = all cores,
+ * capped at 16). Returns the count now in force. No drinkme counterpart
+ * (radix_native.py:220-259 threads in Python instead). */
+int dmx_set_host_threads(int n);
+
+/* Replaces radix_ops.decode_bits (src/drinkme/codec/radix_ops.py:418-427),
+ * the _dense kernel (src/drinkme/codec/radix_kernel_gpu.py:614-636): every
+ * block decoded once to the original u16 bit patterns, out [rows, cols]
+ * (device, row-major). */
+int dmx_radix_decode(const dmx_radix_tensor* t, uint16_t* out, void* stream, char* err, size_t errn);
+
+/* Replaces radix_ops.prepare_schedule (src/drinkme/codec/radix_ops.py:
+ * 341-348), the _prepare_schedule kernel (radix_kernel_gpu.py:44-66):
+ * per block, byte (level - 1) = the word length of nonterminal tier
+ * `level`'s stream, level >= 1. schedule: device, one u16 per block.
+ * Refuses a two-tier tensor (sip has no schedule). */
+int dmx_radix_prepare(const dmx_radix_tensor* t, uint16_t* schedule, void* stream, char* err, size_t errn);
+
+/* Replaces radix_ops.gemv_fused / gemv / gemv_mc (src/drinkme/codec/
+ * radix_ops.py:351-398) — the _gemv, _gemv_mc and _finish kernels
+ * (radix_kernel_gpu.py:682-718, radix_ops.py:91-164).
+ *   x     device [m, cols], x_dtype DMX_BF16 or DMX_F32, row stride cols;
+ *   m     1..8 (ops.MC_MAX, src/drinkme/codec/ops.py:19);
+ *   bias  device [rows] of bias_dtype, or NULL;
+ *   out   device [m, rows] of out_dtype.
+ * out = (x . W^T accumulated in fp32, + bias in fp32) rounded ONCE to
+ * out_dtype (round to nearest even): gemv_fused's epilogue
+ * (src/drinkme/codec/swap.py:284-300). m > 1 with bias NULL and DMX_F32
+ * out is gemv_mc's fp32 [M, R]. */
+int dmx_radix_gemv(const dmx_radix_tensor* t, const void* x, int x_dtype, uint32_t m, const void* bias,
+                   int bias_dtype, void* out, int out_dtype, void* stream, char* err, size_t errn);
+
+/* Kernel choice for dmx_radix_gemv: DMX_POLICY_AUTO or DMX_POLICY_GENERIC
+ * (an A/B switch like DRINKME_RADIX_DECODER, radix_ops.py:286-300).
+ * Returns the previous policy, or -1 for an unknown one. */
+int dmx_radix_set_policy(int policy);
+
+/* Seeded synthetic bf16 weights or activations for the workloads, no
+ * drinkme counterpart: element i of stream (seed, stream) is a function of
+ * i alone (counter-based), so any thread count writes the same bits.
+ * dist 0: N(0, 1) * scale; dist 1: Student-t(nu = 4) / sqrt(2) * scale
+ * (unit variance before the scale). float64 draw -> float32 (nearest) ->
+ * bf16 (nearest even). Host memory. */
+int dmx_synth_bf16(uint64_t seed, uint64_t stream, uint64_t count, double scale, uint32_t dist, uint16_t* out,
+                   char* err, size_t errn);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DMX_RADIX_H */

@@ -1,0 +1,54 @@
+"""GPU parity: the dense decode (dmx_radix_decode) and the schedule
+(dmx_radix_prepare) against the oracle, through the C ABI.
+
+Mirrors drinkme's device gate bench/radix_gemv_bitpin.py:86-116 (all 65,536
+bf16 patterns at every profile, 32- and 1024-weight blocks, bit-exact; the
+schedule equal to the CPU one) and tests/test_radix_bounds.py:149-182 (the
+device reader over a short block = the padded model)."""
+
+import numpy as np
+import pytest
+
+from oracle import radix_oracle as O
+from tests.helpers import all_patterns, finite_bits, oracle_dict, u16_of
+
+pytestmark = pytest.mark.gpu
+
+PROFILES = ("sip", "balanced", "gulp")
+
+
+@pytest.mark.parametrize("profile", PROFILES)
+@pytest.mark.parametrize("block", [32, 1024])
+def test_all_patterns_decode_exactly(cuda, profile, block):
+    from drinkme_amd import radix_ops, swap
+
+    bits = all_patterns()
+    d = oracle_dict(bits, profile, block)
+    rt = swap.to_device_radix(d, cuda)
+    print(f"case all-patterns {profile} B{block}", flush=True)
+    got = u16_of(radix_ops.decode_bits(rt))
+    assert np.array_equal(got, bits)
+    assert np.array_equal(u16_of(radix_ops.decode_bits(rt)), bits)  # deterministic
+    if len(d["widths"]) > 2:
+        want = O.schedule(O.Pack((512, 513), block, tuple(d["widths"]), d["rx_palette"], d["rx_offsets"],
+                                 d["rx_data"]))
+        assert np.array_equal(u16_of(rt["rx_schedule"]), want)
+
+
+@pytest.mark.parametrize("shape", [(1, 1), (7, 33), (3, 1025), (129, 260), (17, 3079), (64, 4096), (8, 12288)])
+@pytest.mark.parametrize("spread", [False, True])
+def test_ragged_and_production_shapes_decode_exactly(cuda, shape, spread):
+    from drinkme_amd import radix_ops, swap
+
+    rng = np.random.default_rng(hash((shape, spread)) % 2**32)
+    bits = finite_bits(rng, shape, spread)
+    for profile in PROFILES:
+        p = O.pack(bits, profile)
+        if p.raw:
+            continue
+        d = oracle_dict(bits, profile)
+        print(f"case ragged {shape} spread={spread} {profile}", flush=True)
+        rt = swap.to_device_radix(d, cuda)
+        assert np.array_equal(u16_of(radix_ops.decode_bits(rt)), bits)
+        if len(d["widths"]) > 2:
+            assert np.array_equal(u16_of(rt["rx_schedule"]), O.schedule(p))

@@ -1,0 +1,155 @@
+"""GPU parity: the fused decode + GEMV (dmx_radix_gemv) against the oracle,
+through the C ABI.
+
+Bars (drinkme's bench/radix_gemv_bitpin.py:181-191, bench/radix_mc_bitpin.py,
+tests/test_codec_bias_rounding.py, and the north star's 1e-2):
+  - fp32 GEMV within the float64 bound 2e-6 |x|.|W| + 1e-7 of the oracle's
+    float64 dot over the source bits;
+  - the fused bf16 output with bias == (fp32 result + bias) rounded once;
+  - every column of an M = 2..8 call within the same bound;
+  - bf16 outputs within 1e-2 relative of decode-then-matmul (fp32
+    accumulate, bf16 out);
+  - the bias cancellation known answer 0.00390625 on every arm.
+"""
+
+import numpy as np
+import pytest
+
+from oracle import radix_oracle as O
+from tests.helpers import bf16_tensor, escape_heavy_bits, finite_bits, oracle_dict, u16_of
+
+pytestmark = pytest.mark.gpu
+
+PROFILES = ("sip", "balanced", "gulp")
+BOUND_TOL = 1.0  # |y - y64| <= bound, the float64 oracle's cancellation-aware bound
+REL_TOL = 1e-2   # the north star's relative tolerance vs decode-then-matmul
+
+
+def _check_bound(y, x_f32, bits, what):
+    ref, bound = O.gemv_f64(bits, x_f32)
+    err = np.abs(np.asarray(y, np.float64) - ref) / bound
+    assert np.all(err <= BOUND_TOL), f"{what}: err/bound {err.max():.3f}"
+    return ref
+
+
+def _run_shape(cuda, bits, profile, rng, ms=(1, 3, 8)):
+    import torch
+
+    from drinkme_amd import radix_ops, swap
+
+    R, C = bits.shape
+    d = oracle_dict(bits, profile)
+    rt = swap.to_device_radix(d, cuda)
+    bias_bits = O.f32_to_bf16_bits(np.linspace(-0.1, 0.1, R).astype(np.float32))
+    bias = bf16_tensor(bias_bits, cuda)
+    for M in ms:
+        xb = O.f32_to_bf16_bits(rng.standard_normal((M, C)).astype(np.float32))
+        x = bf16_tensor(xb, cuda)
+        xf = O.bf16_bits_to_f32(xb)
+        y32 = radix_ops.gemv_rows(rt, x, None, torch.float32).cpu().numpy()
+        _check_bound(y32, xf, bits, f"{profile} {bits.shape} M={M} bf16 x")
+        fused = radix_ops.gemv_rows(rt, x, bias, torch.bfloat16)
+        want = (torch.from_numpy(y32).to(cuda) + bias.float()).to(torch.bfloat16)
+        assert torch.equal(fused, want), f"{profile} {bits.shape} M={M}: fused epilogue"
+        # fp32 activations take the widened path
+        x32 = torch.from_numpy(rng.standard_normal((M, C)).astype(np.float32)).to(cuda)
+        y = radix_ops.gemv_rows(rt, x32, None, torch.float32).cpu().numpy()
+        _check_bound(y, x32.cpu().numpy(), bits, f"{profile} {bits.shape} M={M} fp32 x")
+        # decode-then-matmul: fp32 accumulate over the oracle's decoded weight, bf16 out
+        ref32 = O.gemv_f32(bits, xf, O.bf16_bits_to_f32(bias_bits))
+        got = fused.float().cpu().numpy()
+        want_bf16 = O.bf16_bits_to_f32(O.f32_to_bf16_bits(ref32))
+        scale = np.maximum(np.abs(want_bf16), np.abs(xf) @ np.abs(O.bf16_bits_to_f32(bits)).T * 1e-3 + 1e-6)
+        assert np.all(np.abs(got - want_bf16) <= REL_TOL * scale), f"{profile} {bits.shape} M={M}: 1e-2 relative"
+
+
+@pytest.mark.parametrize("shape", [(1, 1), (7, 33), (3, 1025), (129, 260), (17, 3079)])
+@pytest.mark.parametrize("spread", [False, True])
+@pytest.mark.parametrize("profile", PROFILES)
+def test_ragged_shapes(cuda, shape, spread, profile):
+    rng = np.random.default_rng(abs(hash((shape, spread, profile))) % 2**32)
+    bits = finite_bits(rng, shape, spread)
+    if O.pack(bits, profile).raw:
+        pytest.skip("radix would expand this tensor (stored raw)")
+    print(f"case gemv ragged {shape} spread={spread} {profile}", flush=True)
+    _run_shape(cuda, bits, profile, rng)
+
+
+@pytest.mark.parametrize("shape", [(1024, 4096), (256, 12288), (4096, 1024)])
+@pytest.mark.parametrize("profile", PROFILES)
+def test_production_shapes(cuda, shape, profile):
+    rng = np.random.default_rng(abs(hash((shape, profile))) % 2**32)
+    bits = finite_bits(rng, shape, spread=True)
+    print(f"case gemv production {shape} {profile}", flush=True)
+    _run_shape(cuda, bits, profile, rng, ms=(1, 4))
+
+
+@pytest.mark.parametrize("rate", [0.0, 0.02, 0.1, 0.45])
+def test_sip_fast_path_escape_rates(cuda, rate):
+    """The sip M = 1 kernel across escape densities: none, typical, and a
+    terminal longer than 64 words (> 256 escapes per block)."""
+    import torch
+
+    from drinkme_amd import radix_ops, swap
+
+    rng = np.random.default_rng(int(rate * 1000) + 7)
+    bits = escape_heavy_bits(rng, (512, 4096), rate)
+    d = oracle_dict(bits, "sip")
+    rt = swap.to_device_radix(d, cuda)
+    xb = O.f32_to_bf16_bits(rng.standard_normal((1, 4096)).astype(np.float32))
+    x = bf16_tensor(xb, cuda)
+    print(f"case sip escapes rate={rate}", flush=True)
+    y = radix_ops.gemv(rt, x[0]).cpu().numpy()
+    _check_bound(y[None], O.bf16_bits_to_f32(xb), bits, f"sip escapes {rate}")
+    prev = radix_ops.set_policy("generic")
+    try:
+        yg = radix_ops.gemv(rt, x[0]).cpu().numpy()
+    finally:
+        radix_ops.set_policy(prev)
+    _check_bound(yg[None], O.bf16_bits_to_f32(xb), bits, f"sip escapes {rate} generic")
+    assert torch.cuda.is_available()
+
+
+def test_sip_4096_square(cuda):
+    """The single-linear workload: 4096 x 4096 N(0, 0.02) at sip, x N(0, 1)."""
+    import torch
+
+    from drinkme_amd import radix_ops, radix_pack, swap, synth
+
+    bits = synth.weight("c1", 0, "w", 4096, 4096)
+    p = radix_pack.pack_array_radix(bits, "sip")
+    rt = swap.to_device_radix(p, cuda)
+    assert np.array_equal(u16_of(radix_ops.decode_bits(rt)), bits)
+    xb = synth.activation("c1", "x", 1, 4096)
+    x = bf16_tensor(xb, cuda)
+    y = radix_ops.gemv(rt, x[0]).cpu().numpy()
+    _check_bound(y[None], O.bf16_bits_to_f32(xb), bits, "c1")
+    fused = radix_ops.gemv_fused(rt, x[0], None, torch.bfloat16).float().cpu().numpy()
+    ref32 = O.gemv_f32(bits, O.bf16_bits_to_f32(xb))
+    want = O.bf16_bits_to_f32(O.f32_to_bf16_bits(ref32))
+    rel = np.abs(fused - want) / np.maximum(np.abs(want), 1e-3)
+    assert np.median(rel) < 1e-2 and np.all(np.abs(fused - want) <= 1e-2 * np.maximum(np.abs(want), 0.05))
+
+
+@pytest.mark.parametrize("profile", PROFILES)
+@pytest.mark.parametrize("rows", [1, 4])
+def test_bias_rounds_once(cuda, profile, rows):
+    """W columns 0, 1 = 1, x = [1, 1/256, 0 ...], bias = -1: the fp32
+    accumulator 1.00390625 minus 1 is 2^-8; rounding first would give 0
+    (tests/test_codec_bias_rounding.py:1-19)."""
+    import torch
+
+    from drinkme_amd import swap
+
+    R = C = 1024
+    w = np.zeros((R, C), np.float32)
+    w[:, :2] = 1
+    bits = O.f32_to_bf16_bits(w)
+    d = oracle_dict(bits, profile)
+    mod = swap.make_module(d, torch.full((R,), -1.0, dtype=torch.bfloat16, device=cuda), cuda)
+    x = torch.zeros(rows, C, dtype=torch.bfloat16, device=cuda)
+    x[:, 0] = 1
+    x[:, 1] = 1 / 256
+    assert mod._route(x) == ("gemv" if rows == 1 else "mc")
+    out = mod(x)
+    assert torch.all(out == 0.00390625), out.flatten()[:4]
