@@ -1,0 +1,297 @@
+#!/usr/bin/env python3
+"""Benchmark: drinkme's fused radix decode + GEMV on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
+
+Workloads (seeded synthetic weights, drinkme_amd/synth.py):
+  qwen3-8b-step   (default) one Qwen3-8B decode step's compressed Linears:
+                  36 layers x q/k/v/o/gate/up/down + lm_head = 253 GEMVs,
+                  N(0, 0.02) weights packed at sip, M = 1, bf16 x ~ N(0, 1)
+  qwen3-8b-layer  one such layer (7 GEMVs)
+  linear-4096     one 4096 x 4096 tensor (rotated over 32 packed copies so
+                  the 256 MB last-level cache cannot hold them)
+
+A step is one sweep over the workload's GEMVs, captured once as a HIP graph
+and replayed; inputs are resident in HBM before timing starts. Reported:
+  value       whole-sweep compressed-HBM GB/s = sum of algorithmic bytes /
+              step time, B = 4 NW + 4 (R NB + 1) + 7 + 2 C + 2 R per GEMV
+              (payload, directory, palette, bf16 x and out; not the pad)
+  roofline    the dominant kernel (the 12288 x 4096 gate/up GEMV of the
+              step): its algorithmic bytes per launch / its average launch
+              time, from HIP events around a graph of its launches
+  cpu_baseline  drinkme's CPU route on the host's cores: the compiled
+              drinkme decoder (oracle/_ref) + torch F.linear, on a bounded
+              sample (layer 0), scaled to the step by weight count
+One JSON line goes to stdout; progress lines go to stderr.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_GBPS = 8000.0  # MI355X HBM3E
+PALETTE_BYTES = {"sip": 7, "balanced": 10, "gulp": 21}
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def algorithmic_bytes(rt: dict, m: int = 1) -> int:
+    R, C = int(rt["R"]), int(rt["C"])
+    nb = -(-C // int(rt["block_size"]))
+    return 4 * int(rt["NW"]) + 4 * (R * nb + 1) + PALETTE_BYTES[rt["profile"]] + 2 * m * C + 2 * m * R
+
+
+def workload_items(name: str):
+    from drinkme_amd import synth
+
+    if name == "qwen3-8b-step":
+        return [("qwen3-8b", layer, n, r, c) for layer, n, r, c in synth.qwen3_8b_step()]
+    if name == "qwen3-8b-layer":
+        return [("qwen3-8b", 0, n, r, c) for n, r, c in synth.QWEN3_8B_LAYER]
+    if name == "linear-4096":
+        return [("linear-4096", copy, "w", 4096, 4096) for copy in range(32)]
+    raise SystemExit(f"unknown workload {name!r}")
+
+
+def build_tensors(items, profile: str):
+    import numpy as np  # noqa: F401
+
+    from drinkme_amd import radix_pack, swap, synth
+
+    tensors = []
+    t0 = time.time()
+    last = t0
+    for i, (wl, layer, name, R, C) in enumerate(items):
+        bits = synth.weight(wl, layer, name, R, C)
+        p = radix_pack.pack_array_radix(bits, profile)
+        if p is None:
+            raise SystemExit(f"{wl}/{layer}/{name}: radix would expand this tensor")
+        rt = swap.to_device_radix(p, "cuda")
+        tensors.append({"layer": layer, "name": name, "R": R, "C": C, "rt": rt, "bytes": algorithmic_bytes(rt),
+                        "bf16_bytes": 2 * R * C, "bpw": p["bpw"]})
+        if time.time() - last > 10 or i + 1 == len(items):
+            last = time.time()
+            log(f"packed {i + 1}/{len(items)} tensors ({last - t0:.0f} s)")
+    return tensors
+
+
+def time_graph(fn, replays: int, warmup: int) -> float:
+    """Milliseconds per replay of `fn` captured as a HIP graph."""
+    import torch
+
+    fn()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    for _ in range(warmup):
+        g.replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(replays):
+        g.replay()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / replays
+
+
+def cpu_baseline(tensors, xs, budget_s: float = 12.0):
+    """drinkme's CPU route (src/drinkme/codec/swap.py:344-352): decode the
+    weight with drinkme's compiled C++ decoder (oracle/_ref; the oracle's C
+    decoder when that library is absent), then torch F.linear on the bf16
+    weight. Row ranges decode on all host threads. Sample: layer 0's seven
+    tensors, repeated within `budget_s`; scaled to the whole step by
+    weight count."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    import numpy as np
+    import torch
+
+    from oracle import radix_oracle as O
+
+    kind = "reference" if O.ref_available() else "port"
+    threads = min(os.cpu_count() or 1, 16)
+    torch.set_num_threads(threads)
+    sample = [t for t in tensors if t["layer"] == tensors[0]["layer"]]
+    host = []
+    for t in sample:
+        rt = t["rt"]
+        host.append((rt["rx_palette_np"], rt["rx_offsets"].cpu().numpy(),
+                     rt["rx_data"][: rt["NW"]].cpu().numpy(), t["R"], t["C"], tuple(rt["widths"])))
+    xcpu = {c: x.cpu() for c, x in xs.items()}
+
+    def decode_gemv(h):
+        pal, off, data, R, C, widths = h
+        out = np.empty((R, C), np.uint16)
+        step = -(-R // (4 * threads))
+        if kind == "reference":
+            job = lambda r: O.ref_decode(pal, off, data, R, C, widths, r, min(step, R - r), out[r:])  # noqa: E731
+        else:
+            pk = O.Pack((R, C), 1024, widths, pal, off, data)
+            job = lambda r: O.decode_rows(pk, r, min(step, R - r), out[r:])  # noqa: E731
+        with ThreadPoolExecutor(threads) as ex:
+            list(ex.map(job, range(0, R, step)))
+        W = torch.from_numpy(out.view(np.int16)).view(torch.bfloat16)
+        return torch.nn.functional.linear(xcpu[C], W)
+
+    reps, t0 = 0, time.time()
+    while True:
+        for h in host:
+            decode_gemv(h)
+        reps += 1
+        if time.time() - t0 > budget_s or reps >= 20:
+            break
+    per_sample = (time.time() - t0) / reps
+    sample_w = sum(t["R"] * t["C"] for t in sample)
+    total_w = sum(t["R"] * t["C"] for t in tensors)
+    step_s = per_sample * total_w / sample_w
+    total_bytes = sum(t["bytes"] for t in tensors)
+    return {"value": total_bytes / step_s / 1e9, "unit": "GB/s", "cores": threads, "kind": kind,
+            "sample": f"layer {sample[0]['layer']} ({len(sample)} tensors, {sample_w / 1e6:.0f} M weights) "
+                      f"x{reps}: decode (drinkme C++ decoder, {threads} threads over row ranges) + torch "
+                      f"F.linear bf16 per call; scaled by weight count to the step",
+            "ms_per_step": step_s * 1e3}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--workload", default="qwen3-8b-step",
+                    choices=["qwen3-8b-step", "qwen3-8b-layer", "linear-4096"])
+    ap.add_argument("--profile", default="sip", choices=["sip", "gulp", "balanced"])
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--kernel-only", action="store_true",
+                    help="only the dominant kernel's graph (for counter passes)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU; --gpus {args.gpus} is not supported (this build measures one "
+              "GPU's share: the kernel is row-parallel and would shard by rows, see DESIGN.md)", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from drinkme_amd import radix_ops, synth
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 1
+    items = workload_items(args.workload)
+    if args.kernel_only:
+        items = [it for it in items if (it[3], it[4]) == (12288, 4096)][:16] or items[:8]
+    log(f"workload {args.workload}: {len(items)} GEMVs, profile {args.profile}")
+    tensors = build_tensors(items, args.profile)
+    xs = {}
+    for c in sorted({t["C"] for t in tensors}):
+        xb = synth.activation(args.workload, f"x{c}", 1, c)
+        xs[c] = torch.from_numpy(xb.view("int16")).view(torch.bfloat16).cuda()
+    outs = [torch.empty((1, t["R"]), dtype=torch.bfloat16, device="cuda") for t in tensors]
+    descs = [radix_ops.descriptor(t["rt"]) for t in tensors]
+
+    import ctypes as ct
+
+    from drinkme_amd import _native
+
+    lib = _native.lib()
+    err = _native.error_buffer()
+
+    def launch(i):
+        t = tensors[i]
+        st = lib.dmx_radix_gemv(ct.byref(descs[i]), xs[t["C"]].data_ptr(), _native.DMX_BF16, 1, None, 0,
+                                outs[i].data_ptr(), _native.DMX_BF16,
+                                ct.c_void_p(torch.cuda.current_stream().cuda_stream), err, len(err))
+        if st:
+            raise RuntimeError(err.value.decode())
+
+    def sweep():
+        for i in range(len(tensors)):
+            launch(i)
+
+    dom = [i for i, t in enumerate(tensors) if (t["R"], t["C"]) == (12288, 4096)]
+    if not dom:
+        dom = list(range(len(tensors)))
+
+    def dominant():
+        for i in dom:
+            launch(i)
+
+    total_bytes = sum(t["bytes"] for t in tensors)
+    total_bf16 = sum(t["bf16_bytes"] for t in tensors)
+    dom_ms = time_graph(dominant, max(args.steps, 10), args.warmup)
+    dom_bytes = sum(tensors[i]["bytes"] for i in dom) / len(dom)
+    dom_us = dom_ms * 1e3 / len(dom)
+    achieved = dom_bytes / (dom_us * 1e-6) / 1e9
+    log(f"dominant kernel {tensors[dom[0]]['R']}x{tensors[dom[0]]['C']}: {dom_us:.2f} us/launch, "
+        f"{achieved:.0f} GB/s ({achieved / PEAK_GBPS:.1%} of peak)")
+    if args.kernel_only:
+        # a plain copy of known size beside it: the scale for counter-derived bytes
+        src = torch.empty(64 * 2**20, dtype=torch.float32, device="cuda").fill_(1.0)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log("calibration copy: 3 x 256 MiB device-to-device")
+        return 0
+    ms = time_graph(sweep, args.steps, args.warmup)
+    value = total_bytes / (ms * 1e-3) / 1e9
+    log(f"sweep: {ms * 1e3:.1f} us, {value:.0f} GB/s compressed ({value / PEAK_GBPS:.1%}), "
+        f"{total_bf16 / (ms * 1e-3) / 1e9:.0f} GB/s bf16-equivalent")
+    traffic = None
+    tf = os.path.join(ROOT, "profiles", "traffic.json")
+    key = f"k_gemv_sip {tensors[dom[0]]['R']}x{tensors[dom[0]]['C']} {args.profile} M=1"
+    if os.path.exists(tf):
+        traffic = json.load(open(tf)).get(key, {}).get("hbm_bytes_per_launch")
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("cpu baseline ...")
+        cpu = cpu_baseline(tensors, xs)
+        log(f"cpu baseline: {cpu['value']:.2f} GB/s ({cpu['ms_per_step']:.0f} ms per step, {cpu['cores']} threads)")
+    out = {
+        "metric": "compressed-HBM GB/s of the Qwen3-8B decode-step GEMV sweep (sip, M=1)"
+        if args.workload == "qwen3-8b-step" else f"compressed-HBM GB/s ({args.workload}, {args.profile}, M=1)",
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": args.workload, "profile": args.profile, "m": 1, "gemvs": len(tensors),
+            "weights": sum(t["R"] * t["C"] for t in tensors), "compressed_bytes": total_bytes,
+            "bpw": round(8 * total_bytes / sum(t["R"] * t["C"] for t in tensors), 4),
+            "us_per_sweep": round(ms * 1e3, 2), "pct_of_hbm_peak": round(100 * value / PEAK_GBPS, 2),
+            "effective_bf16_gbps": round(total_bf16 / (ms * 1e-3) / 1e9, 1),
+            "timing": "HIP graph of the sweep, replayed; events around the timed replays",
+            "weights_rng": f"dmx_synth_bf16 seed {synth.SEED}, one stream per (workload, layer, tensor)",
+        },
+        "roofline": {
+            "bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBPS, "unit": "GB/s",
+            "frac": round(achieved / PEAK_GBPS, 4), "traffic": traffic,
+            "kernel": "k_gemv_sip", "shape": f"{tensors[dom[0]]['R']}x{tensors[dom[0]]['C']}",
+            "bytes_per_launch": round(dom_bytes), "us_per_launch": round(dom_us, 3),
+            "launches_timed": len(dom),
+        },
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -29,7 +29,9 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <algorithm>
 #include <atomic>
+#include <cmath>
 
 #include "dmx_radix.h"
 
@@ -262,172 +264,361 @@ __global__ __launch_bounds__(kGenThreads) void k_gemv_generic(Desc d, const void
 
 // ------------------------------------------------- sip, M = 1, whole blocks --
 //
-// Layout: a workgroup of kSipWaves waves takes a tile of kSipWaves / S rows;
-// the S waves of a row split its blocks into contiguous segments and their
-// partial sums meet in LDS. Within a block, lane l owns weights 16l ..
-// 16l + 15: its literals are the 16 bytes at word 4l (one 128-bit load) and
-// its sixteen 3-bit tier-0 codes the 48 bits at bit 48l of the tier-0
-// stream (two words). The activation sits in LDS; so does a per-workgroup
-// table indexed by four codes (12 bits) that gives the exponent fields of
-// the two bf16 pairs they belong to — E(c) << 7 | E(c') << 23, E of the
-// escape code (7) = 0 — and, in the first word's low nibble, the four
-// escape flags. A pair of weights is then one byte-permute of the literals
-// merged (v_bfi) with its table word, and one v_dot2_f32_bf16 with the
-// activation pair.
+// Work split: one resident workgroup of kSipWaves waves per slot (two per
+// CU). Workgroup g owns rows [g T, g T + T); each row is cut into S equal
+// segments of L = NB / S blocks, and the T * S (row, segment) units are
+// dealt to the waves round-robin, so every wave gets the same number of
+// blocks (T, S chosen on the host for that). Unit u covers the workgroup's
+// blocks [u L, u L + L) in row-major order. Each wave streams its blocks with
+// two blocks of loads in flight, sums a unit over its lanes and parks it in
+// LDS; one barrier at the end, then each row's S partials are added in
+// segment order, the bias added, one rounding.
 //
-// Escaped weights: the main pass multiplies their literal with a zero
-// exponent field (|w| < 2^-126, its product below every bound's absolute
-// term for |x| < 2^96). Each lane then walks its own escapes: the rank of
-// an escape in the terminal stream is the wave's exclusive prefix of
-// escape counts (one DPP scan) plus the lane's running count; the
-// terminal's words are staged in the wave's LDS slot, and the exact
-// product x * w is added in fp32.
+// Within a block, lane l owns weights 16l .. 16l + 15: its literals are the
+// 16 bytes at word 4l (one 128-bit load) and its sixteen 3-bit tier-0 codes
+// the 48 bits at bit 48l of the tier-0 stream (two words). Per group of four
+// weights, a 4096-entry LDS table indexed by their four codes gives the
+// exponent fields of the group's two bf16 pairs — E(c) << 7 | E(c') << 23,
+// with E of the escape code (7) = 0 — and, in bits 3..6 of the first word,
+// the group's escape flags m. A pair is then one byte-permute of the
+// literals merged (v_bfi) with its table word, and one v_dot2_f32_bf16 with
+// the activation pair from LDS.
+//
+// Escapes are patched into the exponent words before the products, so every
+// weight is its exact bf16 value. A group's escapes are terminal bytes
+// q .. q + popcount(m) - 1, where q is the wave's exclusive prefix of
+// per-lane escape counts (one DPP scan) plus the lane's earlier groups: the
+// four bytes from q come out of the wave's LDS copy of the terminal stream
+// with one funnel shift, and a 16-entry selector table indexed by m places
+// byte r (the r-th escape of the group) in its pair's exponent field.
 
-constexpr int kSipWaves = 16;
+constexpr int kSipWaves = 12;
 constexpr int kSipThreads = kSipWaves * kWave;
 constexpr uint32_t kSipFixed = 256 + 96;  // literal plane + tier 0 words of a 1024-weight block
 constexpr uint32_t kTableBytes = 4096 * 8;
-constexpr uint32_t kTermWords = 256;  // the widest terminal stream of a block
+constexpr uint32_t kSelBytes = (16 + 9 * 16) * 8;
+constexpr uint32_t kTermWords = 264;  // the widest terminal (256 words) + a window's overhang, per wave
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) void* lds_ptr;
+typedef __attribute__((address_space(1))) void* glb_ptr;
 
 __device__ __forceinline__ float dot2(uint32_t w, uint32_t x, float acc) {
     return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w), __builtin_bit_cast(bf16x2_t, x), acc,
                                            false);
 }
 
-struct SipArgs {
-    const uint32_t* data;
-    const uint32_t* offsets;
-    const uint32_t* palette;
-    const uint16_t* x;
-    const void* bias;
-    void* out;
-    uint32_t rows, cols, nb, segs;
+// Sum over the 64 lanes as an inclusive DPP scan (fixed order); lane 63's
+// value, broadcast.
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+#define DMX_DPP_ADD(ctrl, rmask) \
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), ctrl, rmask, 0xF, false))
+    DMX_DPP_ADD(0x111, 0xF);
+    DMX_DPP_ADD(0x112, 0xF);
+    DMX_DPP_ADD(0x114, 0xF);
+    DMX_DPP_ADD(0x118, 0xF);
+    DMX_DPP_ADD(0x142, 0xA);
+    DMX_DPP_ADD(0x143, 0xC);
+#undef DMX_DPP_ADD
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+
+struct SipShape {
+    uint32_t rows, cols, nb;
+    uint32_t rows_per_wg;  // T
+    uint32_t segs;         // S
+    uint32_t seg_blocks;   // L = NB / S
     int bias_dtype, out_dtype;
 };
 
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
 struct SipStage {
-    uint4 lit;
-    uint32_t t0lo, t0hi, term;
+    u32x4 lit;
+    u32x2 t0;
+    uint32_t term;
     uint32_t start, end;
 };
 
-__device__ __forceinline__ SipStage sip_load(const SipArgs& a, uint32_t blk, uint32_t lane) {
+// A block's directory pair, read through the scalar cache.
+__device__ __forceinline__ uint2 sip_offsets(const uint32_t* __restrict__ offsets, uint32_t blk) {
+    uint2 o;
+    __builtin_memcpy(&o, offsets + blk, 8);
+    return o;
+}
+
+// Per-lane byte offsets of a block's loads: the lane's 16 literal bytes, its
+// two tier-0 words (48 bits at bit 48l) and word l of the terminal region.
+struct SipLanes {
+    uint32_t lit, t0, term;
+};
+
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+
+// A raw buffer resource over [base, base + bytes): 32-bit dword format, no
+// stride, the range checked against `bytes`.
+__device__ __forceinline__ i32x4 make_rsrc(const void* base, uint32_t bytes) {
+    const uint64_t a = reinterpret_cast<uint64_t>(base);
+    i32x4 r;
+    r.x = __builtin_amdgcn_readfirstlane((int32_t)(uint32_t)a);
+    r.y = __builtin_amdgcn_readfirstlane((int32_t)(uint32_t)(a >> 32) & 0xFFFF);
+    r.z = (int32_t)bytes;
+    r.w = 0x00020000;
+    return r;
+}
+
+// A block's loads through the workgroup's buffer resource (based at the
+// workgroup's first block, so every byte offset is small): the terminal
+// word, the tier-0 pair and the literals, issued as one unit of three
+// vector loads. They are written as instructions the compiler does not
+// track, so the only waits on them are the explicit SIP_WAIT below, placed
+// where a stage is consumed: loads return in issue order, so waiting until
+// at most N newer loads are outstanding completes the stage, whatever other
+// loads the compiler adds after it. Every read lies within the block's
+// start + 352 + 64 words, inside block_word_bounds(1024)[1] = 608.
+__device__ __forceinline__ SipStage sip_load(i32x4 rsrc, uint32_t wg_start, uint2 o, const SipLanes& ln) {
     SipStage s;
-    s.start = a.offsets[blk];
-    s.end = a.offsets[blk + 1];
-    const uint32_t* base = a.data + s.start;
-    __builtin_memcpy(&s.lit, base + 4 * lane, 16);
-    const uint32_t w0 = (3 * lane) >> 1;
-    s.t0lo = base[256 + w0];
-    s.t0hi = base[256 + w0 + 1];
-    const uint32_t nterm = s.end > s.start + kSipFixed ? s.end - s.start - kSipFixed : 0;
-    s.term = lane < nterm ? base[kSipFixed + lane] : 0u;
+    s.start = o.x;
+    s.end = o.y;
+    const uint32_t soff = (o.x - wg_start) * 4u;
+    asm volatile(
+        "buffer_load_dword %0, %3, %6, %7 offen\n\t"
+        "buffer_load_dwordx2 %1, %4, %6, %7 offen\n\t"
+        "buffer_load_dwordx4 %2, %5, %6, %7 offen"
+        : "=&v"(s.term), "=&v"(s.t0), "=&v"(s.lit)
+        : "v"(ln.term), "v"(ln.t0), "v"(ln.lit), "s"(rsrc), "s"(soff));
     return s;
 }
 
-__global__ __launch_bounds__(kSipThreads) void k_gemv_sip(SipArgs a) {
-    extern __shared__ __align__(16) uint8_t lds[];
-    uint2* tbl = reinterpret_cast<uint2*>(lds);
-    uint16_t* xs = reinterpret_cast<uint16_t*>(lds + kTableBytes);
-    uint32_t* term_all = reinterpret_cast<uint32_t*>(lds + kTableBytes + 2 * a.cols);
-    float* red = reinterpret_cast<float*>(term_all + kSipWaves * kTermWords);
+// Completes stage S: at most N vector loads issued after it still in flight.
+// The "+v" operands make S's registers this statement's results, so nothing
+// reads them before the wait.
+#define SIP_WAIT(N, S) asm volatile("s_waitcnt vmcnt(" #N ")" : "+v"(S.lit), "+v"(S.t0), "+v"(S.term))
+
+// A wave's place in its work: unit u, block j of the unit, the block's
+// global index and its column block.
+struct SipCursor {
+    uint32_t u, j, blk, cb;
+};
+
+__device__ __forceinline__ void sip_start(const SipShape& sh, SipCursor& c, uint32_t u, uint32_t r0) {
+    c.u = u;
+    c.j = 0;
+    c.blk = r0 * sh.nb + u * sh.seg_blocks;
+    c.cb = (u % sh.segs) * sh.seg_blocks;
+}
+
+__device__ __forceinline__ void sip_next(const SipShape& sh, SipCursor& c, uint32_t r0) {
+    if (++c.j == sh.seg_blocks)
+        sip_start(sh, c, c.u + kSipWaves, r0);
+    else {
+        ++c.blk;
+        ++c.cb;
+    }
+}
+
+__global__ __launch_bounds__(kSipThreads, 6) void k_gemv_sip(const uint32_t* __restrict__ data,
+                                                          const uint32_t* __restrict__ offsets,
+                                                          const uint32_t* __restrict__ palette,
+                                                          const uint16_t* __restrict__ x, const void* __restrict__ bias,
+                                                          void* __restrict__ out, SipShape sh) {
+    // fixed-size tables in static LDS (their addresses fold into the LDS
+    // instructions' offsets); the activation and the row partials after them
+    __shared__ uint2 tbl[4096];
+    __shared__ uint2 sel[16];
+    __shared__ uint2 sel2[9 * 16];
+    __shared__ uint32_t term_all[kSipWaves * kTermWords];
+    extern __shared__ __align__(16) uint8_t lds_dyn[];
+    uint16_t* xs = reinterpret_cast<uint16_t*>(lds_dyn);
+    float* red = reinterpret_cast<float*>(lds_dyn + 2 * sh.cols);
+
+    const uint32_t wv = wave_id(), lane = lane_id();
+    const uint32_t r0 = blockIdx.x * sh.rows_per_wg;
+    const uint32_t nrows = min(sh.rows - r0, sh.rows_per_wg);
+    const uint32_t units = nrows * sh.segs;
+    uint32_t* term = term_all + wv * kTermWords;
+
+    // the activation goes to LDS by direct loads (no registers staged), first
+    // in the queue: small and hot in L2; the barrier below waits for it
+    const uint32_t xchunks = sh.cols / 8;
+    for (uint32_t i = threadIdx.x; i < xchunks; i += kSipThreads)
+        __builtin_amdgcn_global_load_lds((glb_ptr)(reinterpret_cast<const uint4*>(x) + i),
+                                         (lds_ptr)(reinterpret_cast<uint4*>(xs) + (i - lane)), 16, 0, 0);
+
+    // the first two blocks' loads go out before the tables are built; a
+    // cursor past the wave's work reads the workgroup's first block instead
+    const uint32_t first_blk = r0 * sh.nb;
+    SipCursor p, c;
+    sip_start(sh, p, wv, r0);
+    c = p;
+    // the workgroup's payload window: from its first block's first word
+    const uint32_t wg_start = offsets[first_blk];
+    const i32x4 rsrc = make_rsrc(data + wg_start, 0x7FFFFFFFu);
+    SipLanes ln;
+    ln.lit = 16 * lane;
+    ln.t0 = 1024 + 4 * ((3 * lane) >> 1);
+    ln.term = 4 * (kSipFixed + lane);
+    auto next_offsets = [&]() {
+        uint2 o = sip_offsets(offsets, p.u < units ? p.blk : first_blk);
+        sip_next(sh, p, r0);
+        return o;
+    };
+    const uint2 oA = next_offsets(), oB = next_offsets();
+    uint2 oC = next_offsets();
+    // the prologue's two stages issue in the loop's order (no interleaving),
+    // so the waits the loop needs are the same on entry as in steady state
+    SipStage sA = sip_load(rsrc, wg_start, oA, ln);
+    __builtin_amdgcn_sched_barrier(0);
+    SipStage sB = sip_load(rsrc, wg_start, oB, ln);
+    __builtin_amdgcn_sched_barrier(0);
+    SipStage sC;
 
     // the exponent table of this tensor's palette: byte c of the two table
     // words is E(c), byte 7 the zero pad the escape code reads
-    const uint32_t p0 = a.palette[0], p1 = a.palette[1];
+    const uint32_t p0 = palette[0], p1 = palette[1];
     for (uint32_t g = threadIdx.x; g < 4096; g += kSipThreads) {
         uint32_t c0 = g & 7, c1 = (g >> 3) & 7, c2 = (g >> 6) & 7, c3 = (g >> 9) & 7;
         uint32_t e0 = __builtin_amdgcn_perm(p1, p0, c0) & 0xFF, e1 = __builtin_amdgcn_perm(p1, p0, c1) & 0xFF;
         uint32_t e2 = __builtin_amdgcn_perm(p1, p0, c2) & 0xFF, e3 = __builtin_amdgcn_perm(p1, p0, c3) & 0xFF;
-        uint32_t flags = (c0 == 7) | ((c1 == 7) << 1) | ((c2 == 7) << 2) | ((c3 == 7) << 3);
-        tbl[g] = make_uint2((e0 << 7) | (e1 << 23) | flags, (e2 << 7) | (e3 << 23));
+        uint32_t m = (c0 == 7) | ((c1 == 7) << 1) | ((c2 == 7) << 2) | ((c3 == 7) << 3);
+        tbl[g] = make_uint2((e0 << 7) | (e1 << 23) | (m << 3), (e2 << 7) | (e3 << 23));
     }
-    for (uint32_t i = threadIdx.x; i < a.cols / 8; i += kSipThreads)
-        reinterpret_cast<uint4*>(xs)[i] = reinterpret_cast<const uint4*>(a.x)[i];
+    // selectors of escape mask m (4 weights) at offset o: byte 0 / 2 of word
+    // k / 2 picks, for weight k of the group, the window byte of its escape
+    // (o + its rank among the group's escapes), or 0x0C (a zero byte) when
+    // k did not escape. sel: o = 0 (a window per group); sel2[o][m]: one
+    // 8-byte window per lane, o = the lane's escapes in earlier groups.
+    for (uint32_t i = threadIdx.x; i < 9 * 16; i += kSipThreads) {
+        const uint32_t m = i & 15, o = i >> 4;
+        uint32_t b[4];
+        for (uint32_t k = 0, r = o; k < 4; ++k) b[k] = (m >> k) & 1 ? (r++ & 7) : 0x0Cu;
+        const uint2 e = make_uint2(b[0] | 0x0C00u | (b[1] << 16) | 0x0C000000u,
+                                   b[2] | 0x0C00u | (b[3] << 16) | 0x0C000000u);
+        sel2[i] = e;
+        if (o == 0) sel[m] = e;
+    }
+    // every wave's direct loads into LDS must land before any wave reads
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
 
-    const uint32_t wv = wave_id(), lane = lane_id();
-    const uint32_t rows_per_tile = kSipWaves / a.segs;
-    const uint32_t row = blockIdx.x * rows_per_tile + wv / a.segs;
-    const uint32_t seg = wv % a.segs;
-    const uint32_t b0 = seg * a.nb / a.segs, b1 = (seg + 1) * a.nb / a.segs;
-    uint32_t* term = term_all + wv * kTermWords;
-    const uint8_t* term_bytes = reinterpret_cast<const uint8_t*>(term);
+    const uint32_t keep = 0x807F807Fu;  // sign + mantissa bits of a bf16 pair, from the literal
+    float acc0 = 0.0f, acc1 = 0.0f;
+    // one block of the wave's work, from its loaded stage
+    auto process = [&](const SipStage& s0) {
+        const uint64_t v = ((uint64_t)s0.t0.y << 32 | s0.t0.x) >> ((lane & 1) * 16);
+        const uint32_t lo = (uint32_t)v, hi = (uint32_t)(v >> 32);
+        uint2 E0 = tbl[lo & 0xFFF];
+        uint2 E1 = tbl[(lo >> 12) & 0xFFF];
+        uint2 E2 = tbl[__builtin_amdgcn_alignbit(hi, lo, 24) & 0xFFF];
+        uint2 E3 = tbl[(hi >> 4) & 0xFFF];
+        const uint16_t* xb = xs + c.cb * 1024 + 16 * lane;
+        uint4 xa, xc;
+        __builtin_memcpy(&xa, xb, 16);
+        __builtin_memcpy(&xc, xb + 8, 16);
 
-    float acc0 = 0.0f, acc1 = 0.0f, acc_esc = 0.0f;
-    if (row < a.rows && b0 < b1) {
-        SipStage cur = sip_load(a, row * a.nb + b0, lane);
-        for (uint32_t b = b0; b < b1; ++b) {
-            SipStage nxt;
-            if (b + 1 < b1) nxt = sip_load(a, row * a.nb + b + 1, lane);
-
-            const uint64_t v = ((uint64_t)cur.t0hi << 32 | cur.t0lo) >> ((lane & 1) * 16);
-            const uint32_t lo = (uint32_t)v;
-            const uint2 E0 = tbl[lo & 0xFFF];
-            const uint2 E1 = tbl[(lo >> 12) & 0xFFF];
-            const uint2 E2 = tbl[(uint32_t)(v >> 24) & 0xFFF];
-            const uint2 E3 = tbl[(uint32_t)(v >> 36) & 0xFFF];
-            const uint16_t* xb = xs + b * 1024 + 16 * lane;
-            uint4 xa, xc;
-            __builtin_memcpy(&xa, xb, 16);
-            __builtin_memcpy(&xc, xb + 8, 16);
-            const uint32_t keep = 0x807F807Fu;  // sign + mantissa from the literal
-            const uint32_t L0 = cur.lit.x, L1 = cur.lit.y, L2 = cur.lit.z, L3 = cur.lit.w;
-            acc0 = dot2((__builtin_amdgcn_perm(L0, L0, 0x01010000) & keep) | (E0.x & ~keep), xa.x, acc0);
-            acc1 = dot2((__builtin_amdgcn_perm(L0, L0, 0x03030202) & keep) | (E0.y & ~keep), xa.y, acc1);
-            acc0 = dot2((__builtin_amdgcn_perm(L1, L1, 0x01010000) & keep) | (E1.x & ~keep), xa.z, acc0);
-            acc1 = dot2((__builtin_amdgcn_perm(L1, L1, 0x03030202) & keep) | (E1.y & ~keep), xa.w, acc1);
-            acc0 = dot2((__builtin_amdgcn_perm(L2, L2, 0x01010000) & keep) | (E2.x & ~keep), xc.x, acc0);
-            acc1 = dot2((__builtin_amdgcn_perm(L2, L2, 0x03030202) & keep) | (E2.y & ~keep), xc.y, acc1);
-            acc0 = dot2((__builtin_amdgcn_perm(L3, L3, 0x01010000) & keep) | (E3.x & ~keep), xc.z, acc0);
-            acc1 = dot2((__builtin_amdgcn_perm(L3, L3, 0x03030202) & keep) | (E3.y & ~keep), xc.w, acc1);
-
-            // escape flags, one nibble per group of four weights (byte j)
-            const uint32_t m01 = __builtin_amdgcn_perm(E1.x, E0.x, 0x0C0C0400u);
-            const uint32_t m23 = __builtin_amdgcn_perm(E3.x, E2.x, 0x0C0C0400u);
-            uint32_t esc = __builtin_amdgcn_perm(m23, m01, 0x05040100u) & 0x0F0F0F0Fu;
-            const uint32_t cnt = __builtin_popcount(esc);
-            const uint32_t incl = wave_scan_incl(cnt);
-            const uint32_t total = __builtin_amdgcn_readlane(incl, 63);
-            // the terminal is read only when the directory gives the block
-            // words past its fixed streams (radix_kernel_gpu.py:96-98)
-            if (total && cur.end > cur.start + kSipFixed) {
-                const uint32_t need = (total + 3) >> 2;
-                const uint32_t have = min(cur.end - cur.start - kSipFixed, (uint32_t)kWave);
-                term[lane] = cur.term;
-                for (uint32_t j = lane; j < need; j += kWave)
-                    if (j >= have) term[j] = a.data[cur.start + kSipFixed + j];
-                __builtin_amdgcn_wave_barrier();
-                uint32_t q = incl - cnt;
-                while (esc) {
-                    const uint32_t p = __builtin_ctz(esc);
-                    esc &= esc - 1;
-                    const uint32_t grp = p >> 3, k = p & 3;
-                    const uint32_t sel = (((grp & 1) << 2) | k) | 0x0C0C0C00u;
-                    const uint32_t lb = (grp & 2) ? __builtin_amdgcn_perm(L3, L2, sel) : __builtin_amdgcn_perm(L1, L0, sel);
-                    const uint32_t e = term_bytes[q++];
-                    const uint32_t wbits = (__builtin_amdgcn_perm(0u, lb, 0x00000C0Cu) & ~0x7F800000u) | (e << 23);
-                    const float xv = bf16_bits_to_f32(xb[4 * grp + k]);
-                    acc_esc = fmaf(xv, __uint_as_float(wbits), acc_esc);
-                }
-                __builtin_amdgcn_wave_barrier();
-            }
-            cur = nxt;
-        }
+        // escapes: group g's flags are bits 3..6 of E_g.x (a_g = m_g << 3);
+        // a lane's escapes are terminal bytes q0 .. q0 + cnt - 1
+        const uint32_t a0 = E0.x & 0x78u, a1 = E1.x & 0x78u, a2 = E2.x & 0x78u, a3 = E3.x & 0x78u;
+        const uint32_t q1_ = __builtin_popcount(a0), q2_ = q1_ + __builtin_popcount(a1);
+        const uint32_t q3_ = q2_ + __builtin_popcount(a2), cnt = q3_ + __builtin_popcount(a3);
+        const uint32_t q0 = wave_scan_incl(cnt) - cnt;
+        // the terminal is read only when the directory gives the block words
+        // past its fixed streams (radix_kernel_gpu.py:96-98); without it the
+        // escaped exponents stay 0
+        const bool has_term = s0.end > s0.start + kSipFixed;
+        const uint32_t tw = has_term ? s0.term : 0u;  // lane j: terminal word j
+        // common case: every lane's escapes (at most 8) lie in words 0..62
+        if (__builtin_amdgcn_ballot_w64(cnt > 8 || q0 > 243) == 0) {
+            const int k0 = (int)(q0 & ~3u);
+            const uint32_t w0 = __builtin_amdgcn_ds_bpermute(k0, tw);
+            const uint32_t w1 = __builtin_amdgcn_ds_bpermute(k0 + 4, tw);
+            const uint32_t w2 = __builtin_amdgcn_ds_bpermute(k0 + 8, tw);
+            const uint32_t wlo = __builtin_amdgcn_alignbit(w1, w0, q0 << 3);
+            const uint32_t whi = __builtin_amdgcn_alignbit(w2, w1, q0 << 3);
+#define DMX_PATCH2(E, a, off)                                                   \
+    {                                                                           \
+        const uint2 s = sel2[((off) << 4) | ((a) >> 3)];                        \
+        E.x |= __builtin_amdgcn_perm(whi, wlo, s.x) << 7;                       \
+        E.y |= __builtin_amdgcn_perm(whi, wlo, s.y) << 7;                       \
     }
-    const float s = wave_sum(acc0 + acc1 + acc_esc);
-    if (lane == 0) red[wv] = s;
-    __syncthreads();
-    if (threadIdx.x < rows_per_tile) {
-        const uint32_t r = blockIdx.x * rows_per_tile + threadIdx.x;
-        if (r < a.rows) {
-            float sum = 0.0f;
-            for (uint32_t k = 0; k < a.segs; ++k) sum += red[threadIdx.x * a.segs + k];
-            if (a.bias) sum += load_elem(a.bias, a.bias_dtype, r);
-            store_elem(a.out, a.out_dtype, r, sum);
+            DMX_PATCH2(E0, a0, 0)
+            DMX_PATCH2(E1, a1, q1_)
+            DMX_PATCH2(E2, a2, q2_)
+            DMX_PATCH2(E3, a3, q3_)
+#undef DMX_PATCH2
+        } else if (has_term) {
+            // a lane with more than 8 escapes, or more than 243 before it: the
+            // terminal staged in the wave's LDS slot, a window per group
+            const uint32_t total = __builtin_amdgcn_readlane(q0 + cnt, 63);
+            term[lane] = tw;
+            for (uint32_t k = lane + kWave; k < ((total + 3) >> 2) + 2; k += kWave)
+                term[k] = data[s0.start + kSipFixed + k];
+            __builtin_amdgcn_wave_barrier();
+#define DMX_PATCH(E, a, qoff)                                                   \
+    {                                                                           \
+        const uint32_t q = q0 + (qoff);                                         \
+        const uint2 s = sel[(a) >> 3];                                          \
+        const uint32_t* wp = term + (q >> 2);                                   \
+        const uint32_t w = __builtin_amdgcn_alignbit(wp[1], wp[0], q << 3);     \
+        E.x |= __builtin_amdgcn_perm(0u, w, s.x) << 7;                          \
+        E.y |= __builtin_amdgcn_perm(0u, w, s.y) << 7;                          \
+    }
+            DMX_PATCH(E0, a0, 0)
+            DMX_PATCH(E1, a1, q1_)
+            DMX_PATCH(E2, a2, q2_)
+            DMX_PATCH(E3, a3, q3_)
+#undef DMX_PATCH
+            __builtin_amdgcn_wave_barrier();
         }
+        const uint32_t L0 = s0.lit.x, L1 = s0.lit.y, L2 = s0.lit.z, L3 = s0.lit.w;
+        acc0 = dot2((__builtin_amdgcn_perm(L0, L0, 0x01010000) & keep) | (E0.x & ~keep), xa.x, acc0);
+        acc1 = dot2((__builtin_amdgcn_perm(L0, L0, 0x03030202) & keep) | (E0.y & ~keep), xa.y, acc1);
+        acc0 = dot2((__builtin_amdgcn_perm(L1, L1, 0x01010000) & keep) | (E1.x & ~keep), xa.z, acc0);
+        acc1 = dot2((__builtin_amdgcn_perm(L1, L1, 0x03030202) & keep) | (E1.y & ~keep), xa.w, acc1);
+        acc0 = dot2((__builtin_amdgcn_perm(L2, L2, 0x01010000) & keep) | (E2.x & ~keep), xc.x, acc0);
+        acc1 = dot2((__builtin_amdgcn_perm(L2, L2, 0x03030202) & keep) | (E2.y & ~keep), xc.y, acc1);
+        acc0 = dot2((__builtin_amdgcn_perm(L3, L3, 0x01010000) & keep) | (E3.x & ~keep), xc.z, acc0);
+        acc1 = dot2((__builtin_amdgcn_perm(L3, L3, 0x03030202) & keep) | (E3.y & ~keep), xc.w, acc1);
+
+        if (c.j + 1 == sh.seg_blocks) {
+            const float s = wave_sum_dpp(acc0 + acc1);
+            if (lane == 0) red[c.u] = s;
+            acc0 = acc1 = 0.0f;
+        }
+        sip_next(sh, c, r0);
+    };
+    // three stages rotate roles (no register copies); each step issues the
+    // stage two blocks ahead, then completes the oldest (six loads newer);
+    // whole rounds of three blocks, then the remainder
+    const uint32_t my_units = wv < units ? (units - wv + kSipWaves - 1) / kSipWaves : 0;
+    const uint32_t items = my_units * sh.seg_blocks;
+    uint32_t k = 0;
+    for (; k + 3 <= items; k += 3) {
+        sC = sip_load(rsrc, wg_start, oC, ln);
+        uint2 oN = next_offsets();
+        SIP_WAIT(6, sA);
+        process(sA);
+        sA = sip_load(rsrc, wg_start, oN, ln);
+        oN = next_offsets();
+        SIP_WAIT(6, sB);
+        process(sB);
+        sB = sip_load(rsrc, wg_start, oN, ln);
+        oC = next_offsets();
+        SIP_WAIT(6, sC);
+        process(sC);
+    }
+    // in flight now: sA (older), then sB
+    SIP_WAIT(3, sA);
+    if (k < items) process(sA);
+    SIP_WAIT(0, sB);
+    if (k + 1 < items) process(sB);
+    __syncthreads();
+    for (uint32_t t = threadIdx.x; t < nrows; t += kSipThreads) {
+        float sum = 0.0f;
+        for (uint32_t k = 0; k < sh.segs; ++k) sum += red[t * sh.segs + k];
+        if (bias) sum += load_elem(bias, sh.bias_dtype, r0 + t);
+        store_elem(out, sh.out_dtype, r0 + t, sum);
     }
 }
 
@@ -515,34 +706,42 @@ int cu_count() {
 
 int launch_sip(const dmx_radix_tensor* t, const void* x, const void* bias, int bias_dtype, void* out, int out_dtype,
                hipStream_t stream, char* err, size_t errn) {
-    SipArgs a;
-    a.data = t->data;
-    a.offsets = t->offsets;
-    a.palette = t->palette;
-    a.x = static_cast<const uint16_t*>(x);
-    a.bias = bias;
-    a.out = out;
-    a.rows = t->rows;
-    a.cols = t->cols;
-    a.nb = t->cols / 1024;
-    a.bias_dtype = bias_dtype;
-    a.out_dtype = out_dtype;
-    // waves per row: enough row segments that the grid holds ~16 waves per CU
-    const uint64_t want = (uint64_t)cu_count() * 16;
-    uint32_t segs = 1;
-    while (segs < (uint32_t)kSipWaves && segs * 2 <= a.nb && (uint64_t)a.rows * segs < want) segs *= 2;
-    a.segs = segs;
-    const uint32_t rows_per_tile = kSipWaves / segs;
-    const uint32_t grid = (a.rows + rows_per_tile - 1) / rows_per_tile;
-    const size_t lds = kTableBytes + 2 * (size_t)a.cols + kSipWaves * kTermWords * 4 + kSipWaves * 4;
-    static std::atomic<size_t> lds_opted{64 * 1024};
+    SipShape sh;
+    sh.rows = t->rows;
+    sh.cols = t->cols;
+    sh.nb = t->cols / 1024;
+    sh.bias_dtype = bias_dtype;
+    sh.out_dtype = out_dtype;
+    // one workgroup per slot (two per CU), T rows each; S segments per row
+    // so that the T * S units deal evenly to the 16 waves
+    uint32_t grid = std::min<uint32_t>(sh.rows, (uint32_t)cu_count() * 2);
+    sh.rows_per_wg = (sh.rows + grid - 1) / grid;
+    grid = (sh.rows + sh.rows_per_wg - 1) / sh.rows_per_wg;
+    double best = -1.0;
+    sh.segs = 1;
+    for (uint32_t s = 1; s <= std::min<uint32_t>(sh.nb, kSipWaves); ++s) {
+        if (sh.nb % s) continue;
+        const double units = (double)sh.rows_per_wg * s;
+        const double eff = (units / kSipWaves) / std::ceil(units / kSipWaves);
+        if (eff > best + 1e-9) {
+            best = eff;
+            sh.segs = s;
+        }
+    }
+    sh.seg_blocks = sh.nb / sh.segs;
+    const size_t lds = 2 * (size_t)sh.cols + (size_t)sh.rows_per_wg * sh.segs * 4;
+    const size_t fixed = kTableBytes + kSelBytes + kSipWaves * kTermWords * 4;
+    if (lds + fixed > 160 * 1024)
+        return fail(err, errn, "sip gemv: the row tile does not fit in LDS");
+    static std::atomic<size_t> lds_opted{64 * 1024 - fixed};
     if (lds > lds_opted.load()) {
         hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k_gemv_sip),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return fail_hip(err, errn, "sip kernel LDS opt-in", e);
         lds_opted.store(lds);
     }
-    hipLaunchKernelGGL(k_gemv_sip, dim3(grid), dim3(kSipThreads), lds, stream, a);
+    hipLaunchKernelGGL(k_gemv_sip, dim3(grid), dim3(kSipThreads), lds, stream, t->data, t->offsets, t->palette,
+                       static_cast<const uint16_t*>(x), bias, out, sh);
     return launch_check(err, errn, "sip gemv launch");
 }
 

@@ -6,6 +6,8 @@ bf16 patterns at every profile, 32- and 1024-weight blocks, bit-exact; the
 schedule equal to the CPU one) and tests/test_radix_bounds.py:149-182 (the
 device reader over a short block = the padded model)."""
 
+import zlib
+
 import numpy as np
 import pytest
 
@@ -40,7 +42,7 @@ def test_all_patterns_decode_exactly(cuda, profile, block):
 def test_ragged_and_production_shapes_decode_exactly(cuda, shape, spread):
     from drinkme_amd import radix_ops, swap
 
-    rng = np.random.default_rng(hash((shape, spread)) % 2**32)
+    rng = np.random.default_rng(zlib.crc32(repr((shape, spread)).encode()))
     bits = finite_bits(rng, shape, spread)
     for profile in PROFILES:
         p = O.pack(bits, profile)
