@@ -134,9 +134,12 @@ class Pack:
         return self.palette.nbytes + self.offsets.nbytes + self.data.nbytes
 
 
-def pack(bits: np.ndarray, profile: str = "sip", block_size: int = DEFAULT_BLOCK, widths=None) -> Pack:
+def pack(bits: np.ndarray, profile: str = "sip", block_size: int = DEFAULT_BLOCK, widths=None,
+         allow_raw: bool = True) -> Pack:
     """Encode u16 bf16 bit patterns; a tensor that would expand comes back
-    raw (radix.py:77-136). The round trip is checked before returning."""
+    raw (radix.py:77-136) unless allow_raw is False (the encoder's streams
+    whatever their size, as radix_native.cpp's plan + encode write them).
+    The round trip is checked before returning."""
     bits = np.asarray(bits)
     if bits.dtype != np.uint16 or bits.ndim != 2 or min(bits.shape) <= 0:
         raise ValueError("expected a nonempty 2D uint16 array of bf16 bit patterns")
@@ -165,7 +168,7 @@ def pack(bits: np.ndarray, profile: str = "sip", block_size: int = DEFAULT_BLOCK
         raise ValueError(e.value.decode())
     p = Pack((R, C), block_size, widths, palette, offsets, data)
     device = data.nbytes + offsets.nbytes + padded_table_bytes(widths)
-    if max(p.nbytes, device) >= bits.nbytes:
+    if allow_raw and max(p.nbytes, device) >= bits.nbytes:
         p = Pack((R, C), block_size, widths, np.empty(0, np.uint8), np.empty(0, np.uint32),
                  bits.copy(), raw=True)
     if not np.array_equal(decode(p), bits):
