@@ -12,13 +12,18 @@ Workloads (seeded synthetic weights, drinkme_amd/synth.py):
                   the 256 MB last-level cache cannot hold them)
 
 A step is one sweep over the workload's GEMVs, captured once as a HIP graph
-and replayed; inputs are resident in HBM before timing starts. Reported:
+and replayed; inputs are resident in HBM before timing starts. The GEMVs
+that share an activation in a decoder layer (q/k/v; gate/up) run as one
+grouped launch (dmx_radix_gemv_group), the others one launch each; the
+same sweep with one launch per GEMV is timed too (config.ungrouped).
+Reported:
   value       whole-sweep compressed-HBM GB/s = sum of algorithmic bytes /
               step time, B = 4 NW + 4 (R NB + 1) + 7 + 2 C + 2 R per GEMV
               (payload, directory, palette, bf16 x and out; not the pad)
-  roofline    the dominant kernel (the 12288 x 4096 gate/up GEMV of the
-              step): its algorithmic bytes per launch / its average launch
-              time, from HIP events around a graph of its launches
+  roofline    the dominant kernel launch (the grouped gate/up GEMV of a
+              layer, 2 x 12288 x 4096): its algorithmic bytes per launch /
+              its average launch time, from HIP events around a graph of
+              its launches
   cpu_baseline  drinkme's CPU route on the host's cores: the compiled
               drinkme decoder (oracle/_ref) + torch F.linear, on a bounded
               sample (layer 0), scaled to the step by weight count
@@ -189,7 +194,7 @@ def main() -> int:
         return 1
     items = workload_items(args.workload)
     if args.kernel_only:
-        items = [it for it in items if (it[3], it[4]) == (12288, 4096)][:16] or items[:8]
+        items = [it for it in items if it[2] in ("gate", "up")][:16] or items[:8]
     log(f"workload {args.workload}: {len(items)} GEMVs, profile {args.profile}")
     tensors = build_tensors(items, args.profile)
     xs = {}
@@ -206,34 +211,66 @@ def main() -> int:
     lib = _native.lib()
     err = _native.error_buffer()
 
+    # launches: the GEMVs of a layer that share an activation go together
+    share = {"q": "qkv", "k": "qkv", "v": "qkv", "gate": "gateup", "up": "gateup"}
+    groups, last = [], None
+    for i, t in enumerate(tensors):
+        key = (t["layer"], share.get(t["name"]))
+        if key[1] is not None and key == last:
+            groups[-1].append(i)
+        else:
+            groups.append([i])
+        last = key
+    garrs = []
+    for grp in groups:
+        n = len(grp)
+        garrs.append((n, (ct.POINTER(_native.RadixTensor) * n)(*[ct.pointer(descs[i]) for i in grp]),
+                      (ct.c_void_p * n)(*[outs[i].data_ptr() for i in grp]), tensors[grp[0]]["C"]))
+
+    def stream():
+        return ct.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+    def launch_group(gi):
+        n, tarr, oarr, C = garrs[gi]
+        st = lib.dmx_radix_gemv_group(tarr, n, xs[C].data_ptr(), _native.DMX_BF16, 1, None, 0, oarr,
+                                      _native.DMX_BF16, stream(), err, len(err))
+        if st:
+            raise RuntimeError(err.value.decode())
+
     def launch(i):
         t = tensors[i]
         st = lib.dmx_radix_gemv(ct.byref(descs[i]), xs[t["C"]].data_ptr(), _native.DMX_BF16, 1, None, 0,
-                                outs[i].data_ptr(), _native.DMX_BF16,
-                                ct.c_void_p(torch.cuda.current_stream().cuda_stream), err, len(err))
+                                outs[i].data_ptr(), _native.DMX_BF16, stream(), err, len(err))
         if st:
             raise RuntimeError(err.value.decode())
 
     def sweep():
+        for gi in range(len(groups)):
+            launch_group(gi)
+
+    def sweep_ungrouped():
         for i in range(len(tensors)):
             launch(i)
 
-    dom = [i for i, t in enumerate(tensors) if (t["R"], t["C"]) == (12288, 4096)]
+    # the dominant launch: a layer's grouped gate/up (48% of the step's
+    # weights; down is 24%, lm_head 8%); else the largest launch
+    gbytes = [sum(tensors[i]["bytes"] for i in grp) for grp in groups]
+    dom = [gi for gi, grp in enumerate(groups) if sorted(tensors[i]["name"] for i in grp) == ["gate", "up"]]
     if not dom:
-        dom = list(range(len(tensors)))
+        dom = [gbytes.index(max(gbytes))]
+    dom_shape = " + ".join(f"{tensors[i]['R']}x{tensors[i]['C']}" for i in groups[dom[0]])
 
     def dominant():
-        for i in dom:
-            launch(i)
+        for gi in dom:
+            launch_group(gi)
 
     total_bytes = sum(t["bytes"] for t in tensors)
     total_bf16 = sum(t["bf16_bytes"] for t in tensors)
     dom_ms = time_graph(dominant, max(args.steps, 10), args.warmup)
-    dom_bytes = sum(tensors[i]["bytes"] for i in dom) / len(dom)
+    dom_bytes = sum(gbytes[gi] for gi in dom) / len(dom)
     dom_us = dom_ms * 1e3 / len(dom)
     achieved = dom_bytes / (dom_us * 1e-6) / 1e9
-    log(f"dominant kernel {tensors[dom[0]]['R']}x{tensors[dom[0]]['C']}: {dom_us:.2f} us/launch, "
-        f"{achieved:.0f} GB/s ({achieved / PEAK_GBPS:.1%} of peak)")
+    log(f"dominant launch {dom_shape}: {dom_us:.2f} us/launch, {achieved:.0f} GB/s ({achieved / PEAK_GBPS:.1%} of peak)")
     if args.kernel_only:
         # a plain copy of known size beside it: the scale for counter-derived bytes
         src = torch.empty(64 * 2**20, dtype=torch.float32, device="cuda").fill_(1.0)
@@ -245,11 +282,14 @@ def main() -> int:
         return 0
     ms = time_graph(sweep, args.steps, args.warmup)
     value = total_bytes / (ms * 1e-3) / 1e9
-    log(f"sweep: {ms * 1e3:.1f} us, {value:.0f} GB/s compressed ({value / PEAK_GBPS:.1%}), "
+    log(f"sweep ({len(groups)} launches): {ms * 1e3:.1f} us, {value:.0f} GB/s compressed ({value / PEAK_GBPS:.1%}), "
         f"{total_bf16 / (ms * 1e-3) / 1e9:.0f} GB/s bf16-equivalent")
+    ms_u = time_graph(sweep_ungrouped, args.steps, args.warmup)
+    log(f"sweep ungrouped ({len(tensors)} launches): {ms_u * 1e3:.1f} us, "
+        f"{total_bytes / (ms_u * 1e-3) / 1e9:.0f} GB/s compressed")
     traffic = None
     tf = os.path.join(ROOT, "profiles", "traffic.json")
-    key = f"k_gemv_sip {tensors[dom[0]]['R']}x{tensors[dom[0]]['C']} {args.profile} M=1"
+    key = f"k_gemv_sip {dom_shape} {args.profile} M=1"
     if os.path.exists(tf):
         traffic = json.load(open(tf)).get(key, {}).get("hbm_bytes_per_launch")
     cpu = None
@@ -277,13 +317,16 @@ def main() -> int:
             "bpw": round(8 * total_bytes / sum(t["R"] * t["C"] for t in tensors), 4),
             "us_per_sweep": round(ms * 1e3, 2), "pct_of_hbm_peak": round(100 * value / PEAK_GBPS, 2),
             "effective_bf16_gbps": round(total_bf16 / (ms * 1e-3) / 1e9, 1),
+            "launches": len(groups), "grouping": "q/k/v and gate/up of a layer share x: one launch each",
+            "ungrouped": {"launches": len(tensors), "us_per_sweep": round(ms_u * 1e3, 2),
+                          "value": round(total_bytes / (ms_u * 1e-3) / 1e9, 1)},
             "timing": "HIP graph of the sweep, replayed; events around the timed replays",
             "weights_rng": f"dmx_synth_bf16 seed {synth.SEED}, one stream per (workload, layer, tensor)",
         },
         "roofline": {
             "bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBPS, "unit": "GB/s",
             "frac": round(achieved / PEAK_GBPS, 4), "traffic": traffic,
-            "kernel": "k_gemv_sip", "shape": f"{tensors[dom[0]]['R']}x{tensors[dom[0]]['C']}",
+            "kernel": "k_gemv_sip", "shape": dom_shape,
             "bytes_per_launch": round(dom_bytes), "us_per_launch": round(dom_us, 3),
             "launches_timed": len(dom),
         },

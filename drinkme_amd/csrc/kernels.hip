@@ -287,17 +287,19 @@ __global__ __launch_bounds__(kGenThreads) void k_gemv_generic(Desc d, const void
 // Escapes are patched into the exponent words before the products, so every
 // weight is its exact bf16 value. A group's escapes are terminal bytes
 // q .. q + popcount(m) - 1, where q is the wave's exclusive prefix of
-// per-lane escape counts (one DPP scan) plus the lane's earlier groups: the
-// four bytes from q come out of the wave's LDS copy of the terminal stream
-// with one funnel shift, and a 16-entry selector table indexed by m places
-// byte r (the r-th escape of the group) in its pair's exponent field.
+// per-lane escape counts (one DPP scan) plus the lane's earlier groups. Lane
+// j holds terminal word j; when every lane has at most 8 escapes, all below
+// byte 252, a lane pulls its 12-byte window of the terminal with three
+// cross-lane reads (ds_bpermute) and two funnel shifts, and a selector table
+// indexed by (escapes before the group, m) places byte r (the r-th escape
+// of the group) in its pair's exponent field. Otherwise (dense escapes, not
+// seen in trained weights) each group's four bytes are read from memory.
 
 constexpr int kSipWaves = 12;
 constexpr int kSipThreads = kSipWaves * kWave;
 constexpr uint32_t kSipFixed = 256 + 96;  // literal plane + tier 0 words of a 1024-weight block
 constexpr uint32_t kTableBytes = 4096 * 8;
-constexpr uint32_t kSelBytes = (16 + 9 * 16) * 8;
-constexpr uint32_t kTermWords = 264;  // the widest terminal (256 words) + a window's overhang, per wave
+constexpr uint32_t kSelBytes = (16 + 13 * 16) * 8;
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) void* lds_ptr;
@@ -323,13 +325,42 @@ __device__ __forceinline__ float wave_sum_dpp(float v) {
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
 
+// A group of sip tensors that share the activation (the q/k/v or gate/up
+// projections of a layer) runs as one launch: their rows form one row
+// space, tensor i's from row0[i]. The host keeps the row tile no taller than
+// the group's shortest tensor, so a workgroup's rows span at most two
+// tensors; such a workgroup holds both tensors' exponent tables. One tensor
+// is the group of one.
+constexpr int kGroupMax = 4;
+
+struct SipGroup {
+    const uint32_t* data[kGroupMax];
+    const uint32_t* offsets[kGroupMax];
+    const uint32_t* palette[kGroupMax];
+    const void* bias[kGroupMax];
+    void* out[kGroupMax];
+    uint32_t row0[kGroupMax + 1];  // row0[n] = the group's row count
+};
+
 struct SipShape {
-    uint32_t rows, cols, nb;
-    uint32_t rows_per_wg;  // T
-    uint32_t segs;         // S
-    uint32_t seg_blocks;   // L = NB / S
+    uint32_t rows, cols, nb;  // rows of the whole group
+    uint32_t n;               // tensors in the group
+    uint32_t rows_per_wg;     // T
+    uint32_t segs;            // S
+    uint32_t seg_blocks;      // L = NB / S
+    uint32_t tbl2_lds;        // dynamic-LDS byte offset of the second table; 0 = no workgroup spans two tensors
     int bias_dtype, out_dtype;
 };
+
+// arr[i] for a wave-uniform i < kGroupMax, by selects (no indexed copy of
+// the kernel arguments).
+template <typename T>
+__device__ __forceinline__ T pick(const T (&arr)[kGroupMax], uint32_t i) {
+    T v = arr[0];
+#pragma unroll
+    for (int k = 1; k < kGroupMax; ++k) v = i == (uint32_t)k ? arr[k] : v;
+    return v;
+}
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
@@ -339,13 +370,17 @@ struct SipStage {
     u32x2 t0;
     uint32_t term;
     uint32_t start, end;
+    uint32_t t;  // 0: the workgroup's first tensor, 1: its second
 };
 
+// The directory, read-only for the whole launch: through the constant
+// address space its wave-uniform reads become scalar loads.
+typedef const __attribute__((address_space(4))) uint32_t* const_u32_ptr;
+
 // A block's directory pair, read through the scalar cache.
-__device__ __forceinline__ uint2 sip_offsets(const uint32_t* __restrict__ offsets, uint32_t blk) {
-    uint2 o;
-    __builtin_memcpy(&o, offsets + blk, 8);
-    return o;
+__device__ __forceinline__ uint2 sip_offsets(const uint32_t* offsets, uint32_t blk) {
+    const const_u32_ptr p = (const_u32_ptr)(offsets + blk);
+    return make_uint2(p[0], p[1]);
 }
 
 // Per-lane byte offsets of a block's loads: the lane's 16 literal bytes, its
@@ -368,20 +403,21 @@ __device__ __forceinline__ i32x4 make_rsrc(const void* base, uint32_t bytes) {
     return r;
 }
 
-// A block's loads through the workgroup's buffer resource (based at the
-// workgroup's first block, so every byte offset is small): the terminal
-// word, the tier-0 pair and the literals, issued as one unit of three
-// vector loads. They are written as instructions the compiler does not
-// track, so the only waits on them are the explicit SIP_WAIT below, placed
-// where a stage is consumed: loads return in issue order, so waiting until
-// at most N newer loads are outstanding completes the stage, whatever other
-// loads the compiler adds after it. Every read lies within the block's
-// start + 352 + 64 words, inside block_word_bounds(1024)[1] = 608.
-__device__ __forceinline__ SipStage sip_load(i32x4 rsrc, uint32_t wg_start, uint2 o, const SipLanes& ln) {
+// A block's loads through its tensor's buffer resource (based at the
+// workgroup's first block of that tensor, so every byte offset is small):
+// the terminal word, the tier-0 pair and the literals, issued as one unit of
+// three vector loads. They are written as instructions the compiler does
+// not track, so the only waits on them are the explicit SIP_WAIT below,
+// placed where a stage is consumed: loads return in issue order, so waiting
+// until at most N newer loads are outstanding completes the stage, whatever
+// other loads the compiler adds after it. Every read lies within the
+// block's start + 352 + 64 words, inside block_word_bounds(1024)[1] = 608.
+__device__ __forceinline__ SipStage sip_load(i32x4 rsrc, uint32_t base, uint2 o, uint32_t t, const SipLanes& ln) {
     SipStage s;
     s.start = o.x;
     s.end = o.y;
-    const uint32_t soff = (o.x - wg_start) * 4u;
+    s.t = t;
+    const uint32_t soff = (o.x - base) * 4u;
     asm volatile(
         "buffer_load_dword %0, %3, %6, %7 offen\n\t"
         "buffer_load_dwordx2 %1, %4, %6, %7 offen\n\t"
@@ -396,100 +432,164 @@ __device__ __forceinline__ SipStage sip_load(i32x4 rsrc, uint32_t wg_start, uint
 // reads them before the wait.
 #define SIP_WAIT(N, S) asm volatile("s_waitcnt vmcnt(" #N ")" : "+v"(S.lit), "+v"(S.t0), "+v"(S.term))
 
-// A wave's place in its work: unit u, block j of the unit, the block's
-// global index and its column block.
+// A wave's place in its work: unit u, block j of the unit, the block's index
+// in its tensor's directory, its column block, and which of the workgroup's
+// tensors it belongs to.
 struct SipCursor {
-    uint32_t u, j, blk, cb;
+    uint32_t u, j, blk, cb, t;
 };
 
-__device__ __forceinline__ void sip_start(const SipShape& sh, SipCursor& c, uint32_t u, uint32_t r0) {
+// The workgroup's blocks in row-major order: [0, split_blocks) are its
+// first tensor's, from that tensor's block a_first; the rest its second
+// tensor's, from block 0. A unit lies within one row, so within one tensor.
+struct SipSpan {
+    uint32_t a_first, split_blocks;
+};
+
+template <bool TWO>
+__device__ __forceinline__ void sip_start(const SipShape& sh, SipCursor& c, uint32_t u, const SipSpan& sp) {
     c.u = u;
     c.j = 0;
-    c.blk = r0 * sh.nb + u * sh.seg_blocks;
+    const uint32_t wb = u * sh.seg_blocks;
     c.cb = (u % sh.segs) * sh.seg_blocks;
+    c.t = TWO && wb >= sp.split_blocks;
+    c.blk = c.t ? wb - sp.split_blocks : sp.a_first + wb;
 }
 
-__device__ __forceinline__ void sip_next(const SipShape& sh, SipCursor& c, uint32_t r0) {
+template <bool TWO>
+__device__ __forceinline__ void sip_next(const SipShape& sh, SipCursor& c, const SipSpan& sp) {
     if (++c.j == sh.seg_blocks)
-        sip_start(sh, c, c.u + kSipWaves, r0);
+        sip_start<TWO>(sh, c, c.u + kSipWaves, sp);
     else {
         ++c.blk;
         ++c.cb;
     }
 }
 
-__global__ __launch_bounds__(kSipThreads, 6) void k_gemv_sip(const uint32_t* __restrict__ data,
-                                                          const uint32_t* __restrict__ offsets,
-                                                          const uint32_t* __restrict__ palette,
-                                                          const uint16_t* __restrict__ x, const void* __restrict__ bias,
-                                                          void* __restrict__ out, SipShape sh) {
+// Builds the exponent table of a palette: entry g (four 3-bit codes c0..c3)
+// holds E(c0) << 7 | E(c1) << 23 | m << 3 and E(c2) << 7 | E(c3) << 23, where
+// E(7) = 0 (the pad byte) and m = the four escape flags.
+__device__ __forceinline__ void sip_table(uint2* tb, const uint32_t* palette) {
+    const uint32_t p0 = ((const_u32_ptr)palette)[0], p1 = ((const_u32_ptr)palette)[1];
+    // thread h < 512 writes entries 8h .. 8h + 7: c1 c2 c3 = h's codes, c0 = 0..7
+    const uint32_t h = threadIdx.x;
+    if (h < 512) {
+        const uint32_t c1 = h & 7, c2 = (h >> 3) & 7, c3 = h >> 6;
+        const uint32_t y = ((__builtin_amdgcn_perm(p1, p0, c2) & 0xFF) << 7) | ((__builtin_amdgcn_perm(p1, p0, c3) & 0xFF) << 23);
+        const uint32_t xb = ((__builtin_amdgcn_perm(p1, p0, c1) & 0xFF) << 23) |
+                            ((((c1 == 7) << 1) | ((c2 == 7) << 2) | ((c3 == 7) << 3)) << 3);
+#pragma unroll
+        for (uint32_t c0 = 0; c0 < 8; c0 += 2) {
+            const uint32_t e0 = c0 < 4 ? (p0 >> (8 * c0)) & 0xFF : (p1 >> (8 * (c0 - 4))) & 0xFF;
+            const uint32_t e1 = c0 + 1 < 4 ? (p0 >> (8 * (c0 + 1))) & 0xFF : (p1 >> (8 * (c0 - 3))) & 0xFF;
+            const uint4 v = make_uint4(xb | (e0 << 7), y, xb | (e1 << 7) | ((c0 + 1 == 7) << 3), y);
+            *reinterpret_cast<uint4*>(tb + 8 * h + c0) = v;
+        }
+    }
+}
+
+// TWO: some workgroup of the launch spans two tensors (the instantiation
+// without it carries no per-block tensor selects).
+template <bool TWO>
+__global__ __launch_bounds__(kSipThreads, 6) void k_gemv_sip(const SipGroup g, const uint16_t* __restrict__ x,
+                                                          const SipShape sh) {
     // fixed-size tables in static LDS (their addresses fold into the LDS
-    // instructions' offsets); the activation and the row partials after them
+    // instructions' offsets); the activation, the row partials and a second
+    // tensor's table after them
     __shared__ uint2 tbl[4096];
     __shared__ uint2 sel[16];
-    __shared__ uint2 sel2[9 * 16];
-    __shared__ uint32_t term_all[kSipWaves * kTermWords];
+    __shared__ uint2 sel2[13 * 16];
     extern __shared__ __align__(16) uint8_t lds_dyn[];
     uint16_t* xs = reinterpret_cast<uint16_t*>(lds_dyn);
     float* red = reinterpret_cast<float*>(lds_dyn + 2 * sh.cols);
+    uint2* tbl2 = reinterpret_cast<uint2*>(lds_dyn + sh.tbl2_lds);
 
     const uint32_t wv = wave_id(), lane = lane_id();
     const uint32_t r0 = blockIdx.x * sh.rows_per_wg;
     const uint32_t nrows = min(sh.rows - r0, sh.rows_per_wg);
     const uint32_t units = nrows * sh.segs;
-    uint32_t* term = term_all + wv * kTermWords;
+
+    // the workgroup's tensors: ia holds row r0; rows [split, nrows) are ib's
+    uint32_t ia = 0;
+#pragma unroll
+    for (int i = 1; i < kGroupMax; ++i) ia += (uint32_t)i < sh.n && g.row0[i] <= r0;
+    const uint32_t ib = min(ia + 1, sh.n - 1);
+    uint32_t row_a = g.row0[0], row_b = g.row0[1];
+#pragma unroll
+    for (int k = 1; k < kGroupMax; ++k) {
+        row_a = ia == (uint32_t)k ? g.row0[k] : row_a;
+        row_b = ia == (uint32_t)k ? g.row0[k + 1] : row_b;
+    }
+    const uint32_t split = TWO ? min(row_b, r0 + nrows) - r0 : nrows;
+    const bool two = TWO && split < nrows;
+    const uint32_t* data_a = pick(g.data, ia);
+    const uint32_t* data_b = pick(g.data, ib);
+    const uint32_t* offsets_a = pick(g.offsets, ia);
+    const uint32_t* offsets_b = pick(g.offsets, ib);
+    const uint32_t lrow_a = r0 - row_a;
+    SipSpan sp;
+    sp.a_first = lrow_a * sh.nb;
+    sp.split_blocks = split * sh.nb;
 
     // the activation goes to LDS by direct loads (no registers staged), first
-    // in the queue: small and hot in L2; the barrier below waits for it
+    // in the queue: small and hot in L2; the barrier below waits for it.
+    // Within each 1024-column block, 16-byte chunk p < 64 of LDS holds
+    // x[16p .. 16p + 7] and chunk 64 + p holds x[16p + 8 .. 16p + 15], so a
+    // lane's two reads of its 16 activations each cover 1 KB contiguously
+    // over the wave (no bank conflicts).
     const uint32_t xchunks = sh.cols / 8;
-    for (uint32_t i = threadIdx.x; i < xchunks; i += kSipThreads)
-        __builtin_amdgcn_global_load_lds((glb_ptr)(reinterpret_cast<const uint4*>(x) + i),
+    for (uint32_t i = threadIdx.x; i < xchunks; i += kSipThreads) {
+        const uint32_t q = i & 127u, src = (i & ~127u) | (q < 64u ? 2u * q : 2u * (q - 64u) + 1u);
+        __builtin_amdgcn_global_load_lds((glb_ptr)(reinterpret_cast<const uint4*>(x) + src),
                                          (lds_ptr)(reinterpret_cast<uint4*>(xs) + (i - lane)), 16, 0, 0);
+    }
 
     // the first two blocks' loads go out before the tables are built; a
     // cursor past the wave's work reads the workgroup's first block instead
-    const uint32_t first_blk = r0 * sh.nb;
     SipCursor p, c;
-    sip_start(sh, p, wv, r0);
+    sip_start<TWO>(sh, p, wv, sp);
     c = p;
-    // the workgroup's payload window: from its first block's first word
-    const uint32_t wg_start = offsets[first_blk];
-    const i32x4 rsrc = make_rsrc(data + wg_start, 0x7FFFFFFFu);
+    // each tensor's payload window: from the workgroup's first block of it
+    const uint32_t base_a = ((const_u32_ptr)offsets_a)[sp.a_first], base_b = ((const_u32_ptr)offsets_b)[0];
+    const i32x4 rsrc_a = make_rsrc(data_a + base_a, 0x7FFFFFFFu);
+    const i32x4 rsrc_b = make_rsrc(data_b + base_b, 0x7FFFFFFFu);
     SipLanes ln;
     ln.lit = 16 * lane;
     ln.t0 = 1024 + 4 * ((3 * lane) >> 1);
     ln.term = 4 * (kSipFixed + lane);
+    uint32_t nt = 0;  // the tensor of the last next_offsets() block
     auto next_offsets = [&]() {
-        uint2 o = sip_offsets(offsets, p.u < units ? p.blk : first_blk);
-        sip_next(sh, p, r0);
+        const bool live = p.u < units;
+        nt = TWO && live ? p.t : 0u;
+        const uint2 o = sip_offsets(nt ? offsets_b : offsets_a, live ? p.blk : sp.a_first);
+        sip_next<TWO>(sh, p, sp);
         return o;
     };
-    const uint2 oA = next_offsets(), oB = next_offsets();
+    auto load = [&](uint2 o, uint32_t t) {
+        return TWO && t ? sip_load(rsrc_b, base_b, o, 1u, ln) : sip_load(rsrc_a, base_a, o, 0u, ln);
+    };
+    const uint2 oA = next_offsets();
+    const uint32_t tA = nt;
+    const uint2 oB = next_offsets();
+    const uint32_t tB = nt;
     uint2 oC = next_offsets();
-    // the prologue's two stages issue in the loop's order (no interleaving),
+    uint32_t tC = nt;
+    // the prologue's stages issue in the loop's order (no interleaving),
     // so the waits the loop needs are the same on entry as in steady state
-    SipStage sA = sip_load(rsrc, wg_start, oA, ln);
+    SipStage sA = load(oA, tA);
     __builtin_amdgcn_sched_barrier(0);
-    SipStage sB = sip_load(rsrc, wg_start, oB, ln);
+    SipStage sB = load(oB, tB);
     __builtin_amdgcn_sched_barrier(0);
     SipStage sC;
 
-    // the exponent table of this tensor's palette: byte c of the two table
-    // words is E(c), byte 7 the zero pad the escape code reads
-    const uint32_t p0 = palette[0], p1 = palette[1];
-    for (uint32_t g = threadIdx.x; g < 4096; g += kSipThreads) {
-        uint32_t c0 = g & 7, c1 = (g >> 3) & 7, c2 = (g >> 6) & 7, c3 = (g >> 9) & 7;
-        uint32_t e0 = __builtin_amdgcn_perm(p1, p0, c0) & 0xFF, e1 = __builtin_amdgcn_perm(p1, p0, c1) & 0xFF;
-        uint32_t e2 = __builtin_amdgcn_perm(p1, p0, c2) & 0xFF, e3 = __builtin_amdgcn_perm(p1, p0, c3) & 0xFF;
-        uint32_t m = (c0 == 7) | ((c1 == 7) << 1) | ((c2 == 7) << 2) | ((c3 == 7) << 3);
-        tbl[g] = make_uint2((e0 << 7) | (e1 << 23) | (m << 3), (e2 << 7) | (e3 << 23));
-    }
+    sip_table(tbl, pick(g.palette, ia));
+    if (two) sip_table(tbl2, pick(g.palette, ib));
     // selectors of escape mask m (4 weights) at offset o: byte 0 / 2 of word
     // k / 2 picks, for weight k of the group, the window byte of its escape
     // (o + its rank among the group's escapes), or 0x0C (a zero byte) when
     // k did not escape. sel: o = 0 (a window per group); sel2[o][m]: one
     // 8-byte window per lane, o = the lane's escapes in earlier groups.
-    for (uint32_t i = threadIdx.x; i < 9 * 16; i += kSipThreads) {
+    for (uint32_t i = threadIdx.x; i < 13 * 16; i += kSipThreads) {
         const uint32_t m = i & 15, o = i >> 4;
         uint32_t b[4];
         for (uint32_t k = 0, r = o; k < 4; ++k) b[k] = (m >> k) & 1 ? (r++ & 7) : 0x0Cu;
@@ -506,16 +606,17 @@ __global__ __launch_bounds__(kSipThreads, 6) void k_gemv_sip(const uint32_t* __r
     float acc0 = 0.0f, acc1 = 0.0f;
     // one block of the wave's work, from its loaded stage
     auto process = [&](const SipStage& s0) {
+        const uint2* tb = TWO && s0.t ? tbl2 : tbl;
         const uint64_t v = ((uint64_t)s0.t0.y << 32 | s0.t0.x) >> ((lane & 1) * 16);
         const uint32_t lo = (uint32_t)v, hi = (uint32_t)(v >> 32);
-        uint2 E0 = tbl[lo & 0xFFF];
-        uint2 E1 = tbl[(lo >> 12) & 0xFFF];
-        uint2 E2 = tbl[__builtin_amdgcn_alignbit(hi, lo, 24) & 0xFFF];
-        uint2 E3 = tbl[(hi >> 4) & 0xFFF];
-        const uint16_t* xb = xs + c.cb * 1024 + 16 * lane;
+        uint2 E0 = tb[lo & 0xFFF];
+        uint2 E1 = tb[(lo >> 12) & 0xFFF];
+        uint2 E2 = tb[__builtin_amdgcn_alignbit(hi, lo, 24) & 0xFFF];
+        uint2 E3 = tb[(hi >> 4) & 0xFFF];
+        const uint16_t* xb = xs + c.cb * 1024 + 8 * lane;
         uint4 xa, xc;
         __builtin_memcpy(&xa, xb, 16);
-        __builtin_memcpy(&xc, xb + 8, 16);
+        __builtin_memcpy(&xc, xb + 512, 16);
 
         // escapes: group g's flags are bits 3..6 of E_g.x (a_g = m_g << 3);
         // a lane's escapes are terminal bytes q0 .. q0 + cnt - 1
@@ -528,39 +629,44 @@ __global__ __launch_bounds__(kSipThreads, 6) void k_gemv_sip(const uint32_t* __r
         // escaped exponents stay 0
         const bool has_term = s0.end > s0.start + kSipFixed;
         const uint32_t tw = has_term ? s0.term : 0u;  // lane j: terminal word j
-        // common case: every lane's escapes (at most 8) lie in words 0..62
-        if (__builtin_amdgcn_ballot_w64(cnt > 8 || q0 > 243) == 0) {
-            const int k0 = (int)(q0 & ~3u);
-            const uint32_t w0 = __builtin_amdgcn_ds_bpermute(k0, tw);
-            const uint32_t w1 = __builtin_amdgcn_ds_bpermute(k0 + 4, tw);
-            const uint32_t w2 = __builtin_amdgcn_ds_bpermute(k0 + 8, tw);
-            const uint32_t wlo = __builtin_amdgcn_alignbit(w1, w0, q0 << 3);
-            const uint32_t whi = __builtin_amdgcn_alignbit(w2, w1, q0 << 3);
+        // every lane takes the windowed patch, exact where the lane has at
+        // most 8 escapes, all in terminal words 0..62 (the common case); the
+        // window's three words come from the lanes holding them
+        const int k0 = (int)(q0 & ~3u);
+        const uint32_t w0 = __builtin_amdgcn_ds_bpermute(k0, tw);
+        const uint32_t w1 = __builtin_amdgcn_ds_bpermute(k0 + 4, tw);
+        const uint32_t w2 = __builtin_amdgcn_ds_bpermute(k0 + 8, tw);
+        const uint32_t wlo = __builtin_amdgcn_alignbit(w1, w0, q0 << 3);
+        const uint32_t whi = __builtin_amdgcn_alignbit(w2, w1, q0 << 3);
+        // (a lane with up to 16 escapes indexes rows up to 12 of sel2)
 #define DMX_PATCH2(E, a, off)                                                   \
     {                                                                           \
         const uint2 s = sel2[((off) << 4) | ((a) >> 3)];                        \
         E.x |= __builtin_amdgcn_perm(whi, wlo, s.x) << 7;                       \
         E.y |= __builtin_amdgcn_perm(whi, wlo, s.y) << 7;                       \
     }
-            DMX_PATCH2(E0, a0, 0)
-            DMX_PATCH2(E1, a1, q1_)
-            DMX_PATCH2(E2, a2, q2_)
-            DMX_PATCH2(E3, a3, q3_)
+        DMX_PATCH2(E0, a0, 0)
+        DMX_PATCH2(E1, a1, q1_)
+        DMX_PATCH2(E2, a2, q2_)
+        DMX_PATCH2(E3, a3, q3_)
 #undef DMX_PATCH2
-        } else if (has_term) {
-            // a lane with more than 8 escapes, or more than 243 before it: the
-            // terminal staged in the wave's LDS slot, a window per group
-            const uint32_t total = __builtin_amdgcn_readlane(q0 + cnt, 63);
-            term[lane] = tw;
-            for (uint32_t k = lane + kWave; k < ((total + 3) >> 2) + 2; k += kWave)
-                term[k] = data[s0.start + kSipFixed + k];
-            __builtin_amdgcn_wave_barrier();
+        // rare: a lane with more than 8 escapes, or more than 243 before it,
+        // redoes its exponents with each group's four bytes read from the
+        // terminal stream in memory (at most word 352 + 257 of the block:
+        // inside the reach pad). Without a terminal the window was zero and
+        // every lane is already exact.
+        const bool wide = cnt > 8 || q0 > 243;
+        if (__builtin_expect(__builtin_amdgcn_ballot_w64(wide) != 0, 0) && has_term && wide) {
+            E0 = tb[lo & 0xFFF];
+            E1 = tb[(lo >> 12) & 0xFFF];
+            E2 = tb[__builtin_amdgcn_alignbit(hi, lo, 24) & 0xFFF];
+            E3 = tb[(hi >> 4) & 0xFFF];
+            const uint32_t* tp = (TWO && s0.t ? data_b : data_a) + s0.start + kSipFixed;
 #define DMX_PATCH(E, a, qoff)                                                   \
     {                                                                           \
         const uint32_t q = q0 + (qoff);                                         \
         const uint2 s = sel[(a) >> 3];                                          \
-        const uint32_t* wp = term + (q >> 2);                                   \
-        const uint32_t w = __builtin_amdgcn_alignbit(wp[1], wp[0], q << 3);     \
+        const uint32_t w = __builtin_amdgcn_alignbit(tp[(q >> 2) + 1], tp[q >> 2], q << 3); \
         E.x |= __builtin_amdgcn_perm(0u, w, s.x) << 7;                          \
         E.y |= __builtin_amdgcn_perm(0u, w, s.y) << 7;                          \
     }
@@ -569,7 +675,6 @@ __global__ __launch_bounds__(kSipThreads, 6) void k_gemv_sip(const uint32_t* __r
             DMX_PATCH(E2, a2, q2_)
             DMX_PATCH(E3, a3, q3_)
 #undef DMX_PATCH
-            __builtin_amdgcn_wave_barrier();
         }
         const uint32_t L0 = s0.lit.x, L1 = s0.lit.y, L2 = s0.lit.z, L3 = s0.lit.w;
         acc0 = dot2((__builtin_amdgcn_perm(L0, L0, 0x01010000) & keep) | (E0.x & ~keep), xa.x, acc0);
@@ -586,7 +691,7 @@ __global__ __launch_bounds__(kSipThreads, 6) void k_gemv_sip(const uint32_t* __r
             if (lane == 0) red[c.u] = s;
             acc0 = acc1 = 0.0f;
         }
-        sip_next(sh, c, r0);
+        sip_next<TWO>(sh, c, sp);
     };
     // three stages rotate roles (no register copies); each step issues the
     // stage two blocks ahead, then completes the oldest (six loads newer);
@@ -595,16 +700,19 @@ __global__ __launch_bounds__(kSipThreads, 6) void k_gemv_sip(const uint32_t* __r
     const uint32_t items = my_units * sh.seg_blocks;
     uint32_t k = 0;
     for (; k + 3 <= items; k += 3) {
-        sC = sip_load(rsrc, wg_start, oC, ln);
+        sC = load(oC, tC);
         uint2 oN = next_offsets();
+        uint32_t tN = nt;
         SIP_WAIT(6, sA);
         process(sA);
-        sA = sip_load(rsrc, wg_start, oN, ln);
+        sA = load(oN, tN);
         oN = next_offsets();
+        tN = nt;
         SIP_WAIT(6, sB);
         process(sB);
-        sB = sip_load(rsrc, wg_start, oN, ln);
+        sB = load(oN, tN);
         oC = next_offsets();
+        tC = nt;
         SIP_WAIT(6, sC);
         process(sC);
     }
@@ -614,11 +722,19 @@ __global__ __launch_bounds__(kSipThreads, 6) void k_gemv_sip(const uint32_t* __r
     SIP_WAIT(0, sB);
     if (k + 1 < items) process(sB);
     __syncthreads();
+    // each row's segment partials in order, the bias, one rounding
+    const void* bias_a = pick(g.bias, ia);
+    const void* bias_b = pick(g.bias, ib);
+    void* out_a = pick(g.out, ia);
+    void* out_b = pick(g.out, ib);
     for (uint32_t t = threadIdx.x; t < nrows; t += kSipThreads) {
         float sum = 0.0f;
         for (uint32_t k = 0; k < sh.segs; ++k) sum += red[t * sh.segs + k];
-        if (bias) sum += load_elem(bias, sh.bias_dtype, r0 + t);
-        store_elem(out, sh.out_dtype, r0 + t, sum);
+        const bool in_b = t >= split;
+        const uint32_t row = in_b ? t - split : lrow_a + t;
+        const void* bias = in_b ? bias_b : bias_a;
+        if (bias) sum += load_elem(bias, sh.bias_dtype, row);
+        store_elem(in_b ? out_b : out_a, sh.out_dtype, row, sum);
     }
 }
 
@@ -704,44 +820,87 @@ int cu_count() {
     return n;
 }
 
-int launch_sip(const dmx_radix_tensor* t, const void* x, const void* bias, int bias_dtype, void* out, int out_dtype,
-               hipStream_t stream, char* err, size_t errn) {
+// Whether the sip kernel takes tensor t with this activation.
+bool sip_eligible(const dmx_radix_tensor* t, const void* x, int x_dtype, uint32_t m) {
+    return g_policy.load() == DMX_POLICY_AUTO && m == 1 && x_dtype == DMX_BF16 && is_sip(t) && t->block_size == 1024 &&
+           t->cols % 1024 == 0 && (reinterpret_cast<uintptr_t>(x) & 15u) == 0;
+}
+
+// One launch of the sip kernel over n tensors of equal cols (already
+// checked). Returns 2 when the group cannot run as one launch (a row tile
+// taller than a tensor, or tables past the LDS), having launched nothing.
+int launch_sip(const dmx_radix_tensor* const* ts, uint32_t n, const void* x, const void* const* bias, int bias_dtype,
+               void* const* out, int out_dtype, hipStream_t stream, char* err, size_t errn) {
+    if (n < 1 || n > (uint32_t)kGroupMax) return 2;
+    SipGroup g;
     SipShape sh;
-    sh.rows = t->rows;
-    sh.cols = t->cols;
-    sh.nb = t->cols / 1024;
+    uint64_t total = 0;
+    uint32_t min_rows = ts[0]->rows;
+    for (uint32_t i = 0; i < (uint32_t)kGroupMax; ++i) {
+        const dmx_radix_tensor* t = ts[i < n ? i : n - 1];
+        g.data[i] = t->data;
+        g.offsets[i] = t->offsets;
+        g.palette[i] = t->palette;
+        g.bias[i] = bias ? bias[i < n ? i : n - 1] : nullptr;
+        g.out[i] = out[i < n ? i : n - 1];
+        g.row0[i] = (uint32_t)total;
+        if (i < n) {
+            total += t->rows;
+            min_rows = std::min(min_rows, t->rows);
+        }
+    }
+    if (total >= (1ull << 31)) return 2;
+    g.row0[kGroupMax] = (uint32_t)total;
+    for (uint32_t i = n; i <= (uint32_t)kGroupMax; ++i) g.row0[i] = (uint32_t)total;
+    sh.rows = (uint32_t)total;
+    sh.cols = ts[0]->cols;
+    sh.nb = sh.cols / 1024;
+    sh.n = n;
     sh.bias_dtype = bias_dtype;
     sh.out_dtype = out_dtype;
     // one workgroup per slot (two per CU), T rows each; S segments per row
-    // so that the T * S units deal evenly to the 16 waves
+    // so that the T * S units deal evenly to the waves
     uint32_t grid = std::min<uint32_t>(sh.rows, (uint32_t)cu_count() * 2);
     sh.rows_per_wg = (sh.rows + grid - 1) / grid;
+    if (sh.rows_per_wg > min_rows) return 2;
     grid = (sh.rows + sh.rows_per_wg - 1) / sh.rows_per_wg;
-    double best = -1.0;
+    // S: the fewest block-times per workgroup, a unit's closing wave sum
+    // costing about a quarter of a block
+    double best = 1e30;
     sh.segs = 1;
     for (uint32_t s = 1; s <= std::min<uint32_t>(sh.nb, kSipWaves); ++s) {
         if (sh.nb % s) continue;
-        const double units = (double)sh.rows_per_wg * s;
-        const double eff = (units / kSipWaves) / std::ceil(units / kSipWaves);
-        if (eff > best + 1e-9) {
-            best = eff;
+        const double rounds = std::ceil((double)sh.rows_per_wg * s / kSipWaves);
+        const double cost = rounds * ((double)(sh.nb / s) + 0.25);
+        if (cost < best - 1e-9) {
+            best = cost;
             sh.segs = s;
         }
     }
     sh.seg_blocks = sh.nb / sh.segs;
-    const size_t lds = 2 * (size_t)sh.cols + (size_t)sh.rows_per_wg * sh.segs * 4;
-    const size_t fixed = kTableBytes + kSelBytes + kSipWaves * kTermWords * 4;
-    if (lds + fixed > 160 * 1024)
-        return fail(err, errn, "sip gemv: the row tile does not fit in LDS");
+    // a workgroup spans two tensors where a tensor starts inside its tile
+    bool two = false;
+    for (uint32_t i = 1; i < n; ++i) two |= g.row0[i] % sh.rows_per_wg != 0;
+    const size_t head = 2 * (size_t)sh.cols + (((size_t)sh.rows_per_wg * sh.segs * 4 + 15) & ~(size_t)15);
+    sh.tbl2_lds = two ? (uint32_t)head : 0u;
+    const size_t lds = head + (two ? kTableBytes : 0);
+    const size_t fixed = kTableBytes + kSelBytes;
+    if (lds + fixed > 160 * 1024) return 2;
     static std::atomic<size_t> lds_opted{64 * 1024 - fixed};
     if (lds > lds_opted.load()) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(k_gemv_sip),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        if (e != hipSuccess) return fail_hip(err, errn, "sip kernel LDS opt-in", e);
+        for (const void* k : {reinterpret_cast<const void*>(k_gemv_sip<false>),
+                              reinterpret_cast<const void*>(k_gemv_sip<true>)}) {
+            hipError_t e = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+            if (e != hipSuccess) return fail_hip(err, errn, "sip kernel LDS opt-in", e);
+        }
         lds_opted.store(lds);
     }
-    hipLaunchKernelGGL(k_gemv_sip, dim3(grid), dim3(kSipThreads), lds, stream, t->data, t->offsets, t->palette,
-                       static_cast<const uint16_t*>(x), bias, out, sh);
+    if (two)
+        hipLaunchKernelGGL(k_gemv_sip<true>, dim3(grid), dim3(kSipThreads), lds, stream, g,
+                           static_cast<const uint16_t*>(x), sh);
+    else
+        hipLaunchKernelGGL(k_gemv_sip<false>, dim3(grid), dim3(kSipThreads), lds, stream, g,
+                           static_cast<const uint16_t*>(x), sh);
     return launch_check(err, errn, "sip gemv launch");
 }
 
@@ -750,6 +909,35 @@ void launch_generic_m(const Desc& d, const void* x, int x_dtype, const void* bia
                       int out_dtype, hipStream_t stream) {
     hipLaunchKernelGGL(k_gemv_generic<M>, dim3(d.rows), dim3(kGenThreads), 0, stream, d, x, x_dtype, bias, bias_dtype,
                        out, out_dtype);
+}
+
+int check_gemv_args(const void* x, int x_dtype, uint32_t m, const void* bias, int bias_dtype, const void* out,
+                    int out_dtype, char* err, size_t errn) {
+    if (!x || !out) return fail(err, errn, "null activation or output");
+    if (m < 1 || m > 8) return fail(err, errn, "m outside 1..8");
+    if ((x_dtype != DMX_BF16 && x_dtype != DMX_F32) || (out_dtype != DMX_BF16 && out_dtype != DMX_F32) ||
+        (bias && bias_dtype != DMX_BF16 && bias_dtype != DMX_F32))
+        return fail(err, errn, "dtype must be DMX_BF16 or DMX_F32");
+    return 0;
+}
+
+int gemv_one(const dmx_radix_tensor* t, const Desc& d, const void* x, int x_dtype, uint32_t m, const void* bias,
+             int bias_dtype, void* out, int out_dtype, hipStream_t s, char* err, size_t errn) {
+    if (sip_eligible(t, x, x_dtype, m)) {
+        const int rc = launch_sip(&t, 1, x, &bias, bias_dtype, &out, out_dtype, s, err, errn);
+        if (rc != 2) return rc;
+    }
+    switch (m) {
+        case 1: launch_generic_m<1>(d, x, x_dtype, bias, bias_dtype, out, out_dtype, s); break;
+        case 2: launch_generic_m<2>(d, x, x_dtype, bias, bias_dtype, out, out_dtype, s); break;
+        case 3: launch_generic_m<3>(d, x, x_dtype, bias, bias_dtype, out, out_dtype, s); break;
+        case 4: launch_generic_m<4>(d, x, x_dtype, bias, bias_dtype, out, out_dtype, s); break;
+        case 5: launch_generic_m<5>(d, x, x_dtype, bias, bias_dtype, out, out_dtype, s); break;
+        case 6: launch_generic_m<6>(d, x, x_dtype, bias, bias_dtype, out, out_dtype, s); break;
+        case 7: launch_generic_m<7>(d, x, x_dtype, bias, bias_dtype, out, out_dtype, s); break;
+        default: launch_generic_m<8>(d, x, x_dtype, bias, bias_dtype, out, out_dtype, s); break;
+    }
+    return launch_check(err, errn, "generic gemv launch");
 }
 
 }  // namespace
@@ -788,25 +976,40 @@ extern "C" int dmx_radix_gemv(const dmx_radix_tensor* t, const void* x, int x_dt
                               int bias_dtype, void* out, int out_dtype, void* stream, char* err, size_t errn) {
     Desc d;
     if (check_tensor(t, d, err, errn)) return 1;
-    if (!x || !out) return fail(err, errn, "null activation or output");
-    if (m < 1 || m > 8) return fail(err, errn, "m outside 1..8");
-    if ((x_dtype != DMX_BF16 && x_dtype != DMX_F32) || (out_dtype != DMX_BF16 && out_dtype != DMX_F32) ||
-        (bias && bias_dtype != DMX_BF16 && bias_dtype != DMX_F32))
-        return fail(err, errn, "dtype must be DMX_BF16 or DMX_F32");
-    hipStream_t s = static_cast<hipStream_t>(stream);
-    const bool aligned = (reinterpret_cast<uintptr_t>(x) & 15u) == 0;
-    if (g_policy.load() == DMX_POLICY_AUTO && m == 1 && x_dtype == DMX_BF16 && is_sip(t) && t->block_size == 1024 &&
-        t->cols % 1024 == 0 && aligned)
-        return launch_sip(t, x, bias, bias_dtype, out, out_dtype, s, err, errn);
-    switch (m) {
-        case 1: launch_generic_m<1>(d, x, x_dtype, bias, bias_dtype, out, out_dtype, s); break;
-        case 2: launch_generic_m<2>(d, x, x_dtype, bias, bias_dtype, out, out_dtype, s); break;
-        case 3: launch_generic_m<3>(d, x, x_dtype, bias, bias_dtype, out, out_dtype, s); break;
-        case 4: launch_generic_m<4>(d, x, x_dtype, bias, bias_dtype, out, out_dtype, s); break;
-        case 5: launch_generic_m<5>(d, x, x_dtype, bias, bias_dtype, out, out_dtype, s); break;
-        case 6: launch_generic_m<6>(d, x, x_dtype, bias, bias_dtype, out, out_dtype, s); break;
-        case 7: launch_generic_m<7>(d, x, x_dtype, bias, bias_dtype, out, out_dtype, s); break;
-        default: launch_generic_m<8>(d, x, x_dtype, bias, bias_dtype, out, out_dtype, s); break;
+    if (check_gemv_args(x, x_dtype, m, bias, bias_dtype, out, out_dtype, err, errn)) return 1;
+    return gemv_one(t, d, x, x_dtype, m, bias, bias_dtype, out, out_dtype, static_cast<hipStream_t>(stream), err,
+                    errn);
+}
+
+extern "C" int dmx_radix_gemv_group(const dmx_radix_tensor* const* tensors, uint32_t n, const void* x, int x_dtype,
+                                    uint32_t m, const void* const* bias, int bias_dtype, void* const* out,
+                                    int out_dtype, void* stream, char* err, size_t errn) {
+    if (!tensors || !out || n == 0) return fail(err, errn, "empty tensor group");
+    Desc d[kGroupMax];
+    bool one_launch = n <= (uint32_t)kGroupMax;
+    for (uint32_t i = 0; i < n; ++i) {
+        Desc di;
+        if (check_tensor(tensors[i], di, err, errn)) return 1;
+        if (tensors[i]->cols != tensors[0]->cols) return fail(err, errn, "a tensor group must share cols (one activation)");
+        if (check_gemv_args(x, x_dtype, m, bias ? bias[i] : nullptr, bias_dtype, out[i], out_dtype, err, errn))
+            return 1;
+        one_launch = one_launch && sip_eligible(tensors[i], x, x_dtype, m);
+        if (i < (uint32_t)kGroupMax) d[i] = di;
     }
-    return launch_check(err, errn, "generic gemv launch");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (one_launch) {
+        const int rc = launch_sip(tensors, n, x, bias, bias_dtype, out, out_dtype, s, err, errn);
+        if (rc != 2) return rc;
+    }
+    for (uint32_t i = 0; i < n; ++i) {
+        Desc di;
+        if (i < (uint32_t)kGroupMax)
+            di = d[i];
+        else
+            check_tensor(tensors[i], di, err, errn);
+        if (gemv_one(tensors[i], di, x, x_dtype, m, bias ? bias[i] : nullptr, bias_dtype, out[i], out_dtype, s, err,
+                     errn))
+            return 1;
+    }
+    return 0;
 }

@@ -108,6 +108,54 @@ def gemv_mc(p: dict, x: torch.Tensor) -> torch.Tensor:
     return gemv_rows(p, x, None, torch.float32)
 
 
+def gemv_group(ps, x: torch.Tensor, biases=None, out_dtype=torch.bfloat16) -> list:
+    """Several radix tensors that share the activation (a layer's q/k/v or
+    gate/up): x [M, C] or [C] -> one [M, R_i] output per tensor, each as
+    gemv_rows would give it (within the same float64 bound), as one launch
+    where the kernels allow (dmx_radix_gemv_group). No drinkme counterpart:
+    drinkme launches one GEMV per Linear."""
+    ps = list(ps)
+    if not ps:
+        raise ValueError("radix gemv_group: no tensors")
+    if x.dim() == 1:
+        x = x.reshape(1, -1)
+    C = int(ps[0]["C"])
+    if x.dim() != 2 or x.shape[1] != C or any(int(p["C"]) != C for p in ps):
+        raise ValueError(f"radix gemv_group: every tensor needs C = {C} and x [M, {C}]")
+    M = x.shape[0]
+    if not 1 <= M <= MC_MAX:
+        raise ValueError(f"radix gemv_group: M={M} outside 1..{MC_MAX}")
+    if any(x.device != p["rx_data"].device for p in ps):
+        raise ValueError("radix gemv_group: x is not on the weights' device")
+    x = x.contiguous()
+    xd = _dtype_code(x.dtype, "activation")
+    od = _dtype_code(out_dtype, "output")
+    outs = [torch.empty((M, int(p["R"])), dtype=out_dtype, device=x.device) for p in ps]
+    n = len(ps)
+    bias_arr, bd = None, 0
+    if biases is not None:
+        biases = [None if b is None else b.contiguous() for b in biases]
+        if len(biases) != n:
+            raise ValueError("radix gemv_group: one bias (or None) per tensor")
+        dts = {b.dtype for b in biases if b is not None}
+        if len(dts) > 1:
+            raise ValueError("radix gemv_group: the biases must share a dtype")
+        for b, p in zip(biases, ps):
+            if b is not None and (b.numel() != int(p["R"]) or b.device != x.device):
+                raise ValueError("radix gemv_group: bias must hold R elements on the weight's device")
+        if dts:
+            bd = _dtype_code(dts.pop(), "bias")
+        bias_arr = (ct.c_void_p * n)(*[None if b is None else b.data_ptr() for b in biases])
+    descs = [descriptor(p) for p in ps]
+    tarr = (ct.POINTER(_native.RadixTensor) * n)(*[ct.pointer(d) for d in descs])
+    oarr = (ct.c_void_p * n)(*[o.data_ptr() for o in outs])
+    err = _native.error_buffer()
+    st = _native.lib().dmx_radix_gemv_group(tarr, n, x.data_ptr(), xd, M, bias_arr, bd, oarr, od, _stream(), err,
+                                             len(err))
+    _native.check(st, err, "dmx_radix_gemv_group")
+    return outs
+
+
 def decode_bits(p: dict, num_warps: int | None = None) -> torch.Tensor:
     """Every block once -> the original u16 bit patterns [R, C]
     (radix_ops.py:418-427). `num_warps` is accepted for the signature and

@@ -121,6 +121,21 @@ int dmx_radix_prepare(const dmx_radix_tensor* t, uint16_t* schedule, void* strea
 int dmx_radix_gemv(const dmx_radix_tensor* t, const void* x, int x_dtype, uint32_t m, const void* bias,
                    int bias_dtype, void* out, int out_dtype, void* stream, char* err, size_t errn);
 
+/* dmx_radix_gemv over n tensors that share one activation x (the q/k/v or
+ * gate/up projections of a layer), as one launch where the kernels allow:
+ * out[i] = dmx_radix_gemv(tensors[i], x, ..., bias ? bias[i] : NULL, out[i]).
+ * Every tensor has the same cols; bias is NULL or n pointers (each may be
+ * NULL). Each output is within the same bound of the float64 dot as
+ * dmx_radix_gemv's, though its fp32 summation order may differ. No drinkme
+ * counterpart: drinkme launches radix_ops.gemv_fused once per Linear
+ * (src/drinkme/codec/swap.py:443-456); this is the grouped launch that
+ * removes the per-launch cost from the decode step. Refuses (launching
+ * nothing) on any tensor or argument dmx_radix_gemv refuses, or on unequal
+ * cols. */
+int dmx_radix_gemv_group(const dmx_radix_tensor* const* tensors, uint32_t n, const void* x, int x_dtype, uint32_t m,
+                         const void* const* bias, int bias_dtype, void* const* out, int out_dtype, void* stream,
+                         char* err, size_t errn);
+
 /* Kernel choice for dmx_radix_gemv: DMX_POLICY_AUTO or DMX_POLICY_GENERIC
  * (an A/B switch like DRINKME_RADIX_DECODER, radix_ops.py:286-300).
  * Returns the previous policy, or -1 for an unknown one. */
