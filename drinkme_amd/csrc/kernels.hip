@@ -349,6 +349,7 @@ struct SipShape {
     uint32_t segs;            // S
     uint32_t seg_blocks;      // L = NB / S
     uint32_t tbl2_lds;        // dynamic-LDS byte offset of the second table; 0 = no workgroup spans two tensors
+    uint32_t m;               // activation rows (<= the kernel's M; rows past m are padding)
     int bias_dtype, out_dtype;
 };
 
@@ -489,9 +490,13 @@ __device__ __forceinline__ void sip_table(uint2* tb, const uint32_t* palette) {
 }
 
 // TWO: some workgroup of the launch spans two tensors (the instantiation
-// without it carries no per-block tensor selects).
-template <bool TWO>
-__global__ __launch_bounds__(kSipThreads, 6) void k_gemv_sip(const SipGroup g, const uint16_t* __restrict__ x,
+// without it carries no per-block tensor selects). M: activation rows, 1, 2,
+// 4 or 8 (sh.m of them real); each decoded weight pair meets the M rows in
+// turn, so the decode is paid once per block whatever M is.
+// (M = 8 holds one workgroup per CU: its activation rows alone take 8 * 2 *
+// cols bytes of LDS, so it is given the registers of 3 waves per SIMD.)
+template <bool TWO, int M>
+__global__ __launch_bounds__(kSipThreads, M == 8 ? 3 : 6) void k_gemv_sip(const SipGroup g, const uint16_t* __restrict__ x,
                                                           const SipShape sh) {
     // fixed-size tables in static LDS (their addresses fold into the LDS
     // instructions' offsets); the activation, the row partials and a second
@@ -501,7 +506,7 @@ __global__ __launch_bounds__(kSipThreads, 6) void k_gemv_sip(const SipGroup g, c
     __shared__ uint2 sel2[13 * 16];
     extern __shared__ __align__(16) uint8_t lds_dyn[];
     uint16_t* xs = reinterpret_cast<uint16_t*>(lds_dyn);
-    float* red = reinterpret_cast<float*>(lds_dyn + 2 * sh.cols);
+    float* red = reinterpret_cast<float*>(lds_dyn + 2 * M * sh.cols);
     uint2* tbl2 = reinterpret_cast<uint2*>(lds_dyn + sh.tbl2_lds);
 
     const uint32_t wv = wave_id(), lane = lane_id();
@@ -537,9 +542,12 @@ __global__ __launch_bounds__(kSipThreads, 6) void k_gemv_sip(const SipGroup g, c
     // x[16p .. 16p + 7] and chunk 64 + p holds x[16p + 8 .. 16p + 15], so a
     // lane's two reads of its 16 activations each cover 1 KB contiguously
     // over the wave (no bank conflicts).
+    // Row m of x sits at xs + m * cols; a padding row (m >= sh.m) repeats
+    // the last real row (its sums are never stored).
     const uint32_t xchunks = sh.cols / 8;
-    for (uint32_t i = threadIdx.x; i < xchunks; i += kSipThreads) {
-        const uint32_t q = i & 127u, src = (i & ~127u) | (q < 64u ? 2u * q : 2u * (q - 64u) + 1u);
+    for (uint32_t i = threadIdx.x; i < M * xchunks; i += kSipThreads) {
+        const uint32_t m = i / xchunks, j = i - m * xchunks, q = j & 127u;
+        const uint32_t src = min(m, sh.m - 1) * xchunks + ((j & ~127u) | (q < 64u ? 2u * q : 2u * (q - 64u) + 1u));
         __builtin_amdgcn_global_load_lds((glb_ptr)(reinterpret_cast<const uint4*>(x) + src),
                                          (lds_ptr)(reinterpret_cast<uint4*>(xs) + (i - lane)), 16, 0, 0);
     }
@@ -603,7 +611,11 @@ __global__ __launch_bounds__(kSipThreads, 6) void k_gemv_sip(const SipGroup g, c
     __syncthreads();
 
     const uint32_t keep = 0x807F807Fu;  // sign + mantissa bits of a bf16 pair, from the literal
+    // M = 1 keeps two accumulator chains; M > 1 one per row
     float acc0 = 0.0f, acc1 = 0.0f;
+    float acc[M];
+#pragma unroll
+    for (int m = 0; m < M; ++m) acc[m] = 0.0f;
     // one block of the wave's work, from its loaded stage
     auto process = [&](const SipStage& s0) {
         const uint2* tb = TWO && s0.t ? tbl2 : tbl;
@@ -615,8 +627,10 @@ __global__ __launch_bounds__(kSipThreads, 6) void k_gemv_sip(const SipGroup g, c
         uint2 E3 = tb[(hi >> 4) & 0xFFF];
         const uint16_t* xb = xs + c.cb * 1024 + 8 * lane;
         uint4 xa, xc;
-        __builtin_memcpy(&xa, xb, 16);
-        __builtin_memcpy(&xc, xb + 512, 16);
+        if (M == 1) {
+            __builtin_memcpy(&xa, xb, 16);
+            __builtin_memcpy(&xc, xb + 512, 16);
+        }
 
         // escapes: group g's flags are bits 3..6 of E_g.x (a_g = m_g << 3);
         // a lane's escapes are terminal bytes q0 .. q0 + cnt - 1
@@ -677,19 +691,55 @@ __global__ __launch_bounds__(kSipThreads, 6) void k_gemv_sip(const SipGroup g, c
 #undef DMX_PATCH
         }
         const uint32_t L0 = s0.lit.x, L1 = s0.lit.y, L2 = s0.lit.z, L3 = s0.lit.w;
-        acc0 = dot2((__builtin_amdgcn_perm(L0, L0, 0x01010000) & keep) | (E0.x & ~keep), xa.x, acc0);
-        acc1 = dot2((__builtin_amdgcn_perm(L0, L0, 0x03030202) & keep) | (E0.y & ~keep), xa.y, acc1);
-        acc0 = dot2((__builtin_amdgcn_perm(L1, L1, 0x01010000) & keep) | (E1.x & ~keep), xa.z, acc0);
-        acc1 = dot2((__builtin_amdgcn_perm(L1, L1, 0x03030202) & keep) | (E1.y & ~keep), xa.w, acc1);
-        acc0 = dot2((__builtin_amdgcn_perm(L2, L2, 0x01010000) & keep) | (E2.x & ~keep), xc.x, acc0);
-        acc1 = dot2((__builtin_amdgcn_perm(L2, L2, 0x03030202) & keep) | (E2.y & ~keep), xc.y, acc1);
-        acc0 = dot2((__builtin_amdgcn_perm(L3, L3, 0x01010000) & keep) | (E3.x & ~keep), xc.z, acc0);
-        acc1 = dot2((__builtin_amdgcn_perm(L3, L3, 0x03030202) & keep) | (E3.y & ~keep), xc.w, acc1);
+        uint32_t wp[8];
+        wp[0] = (__builtin_amdgcn_perm(L0, L0, 0x01010000) & keep) | (E0.x & ~keep);
+        wp[1] = (__builtin_amdgcn_perm(L0, L0, 0x03030202) & keep) | (E0.y & ~keep);
+        wp[2] = (__builtin_amdgcn_perm(L1, L1, 0x01010000) & keep) | (E1.x & ~keep);
+        wp[3] = (__builtin_amdgcn_perm(L1, L1, 0x03030202) & keep) | (E1.y & ~keep);
+        wp[4] = (__builtin_amdgcn_perm(L2, L2, 0x01010000) & keep) | (E2.x & ~keep);
+        wp[5] = (__builtin_amdgcn_perm(L2, L2, 0x03030202) & keep) | (E2.y & ~keep);
+        wp[6] = (__builtin_amdgcn_perm(L3, L3, 0x01010000) & keep) | (E3.x & ~keep);
+        wp[7] = (__builtin_amdgcn_perm(L3, L3, 0x03030202) & keep) | (E3.y & ~keep);
+        if (M == 1) {
+            acc0 = dot2(wp[0], xa.x, acc0);
+            acc1 = dot2(wp[1], xa.y, acc1);
+            acc0 = dot2(wp[2], xa.z, acc0);
+            acc1 = dot2(wp[3], xa.w, acc1);
+            acc0 = dot2(wp[4], xc.x, acc0);
+            acc1 = dot2(wp[5], xc.y, acc1);
+            acc0 = dot2(wp[6], xc.z, acc0);
+            acc1 = dot2(wp[7], xc.w, acc1);
+        } else {
+#pragma unroll
+            for (int m = 0; m < M; ++m) {
+                uint4 ya, yc;
+                __builtin_memcpy(&ya, xb + m * sh.cols, 16);
+                __builtin_memcpy(&yc, xb + m * sh.cols + 512, 16);
+                float a = acc[m];
+                a = dot2(wp[0], ya.x, a);
+                a = dot2(wp[1], ya.y, a);
+                a = dot2(wp[2], ya.z, a);
+                a = dot2(wp[3], ya.w, a);
+                a = dot2(wp[4], yc.x, a);
+                a = dot2(wp[5], yc.y, a);
+                a = dot2(wp[6], yc.z, a);
+                acc[m] = dot2(wp[7], yc.w, a);
+            }
+        }
 
         if (c.j + 1 == sh.seg_blocks) {
-            const float s = wave_sum_dpp(acc0 + acc1);
-            if (lane == 0) red[c.u] = s;
-            acc0 = acc1 = 0.0f;
+            if (M == 1) {
+                const float s = wave_sum_dpp(acc0 + acc1);
+                if (lane == 0) red[c.u] = s;
+                acc0 = acc1 = 0.0f;
+            } else {
+#pragma unroll
+                for (int m = 0; m < M; ++m) {
+                    const float s = wave_sum_dpp(acc[m]);
+                    if (lane == 0) red[c.u * M + m] = s;
+                    acc[m] = 0.0f;
+                }
+            }
         }
         sip_next<TWO>(sh, c, sp);
     };
@@ -722,19 +772,25 @@ __global__ __launch_bounds__(kSipThreads, 6) void k_gemv_sip(const SipGroup g, c
     SIP_WAIT(0, sB);
     if (k + 1 < items) process(sB);
     __syncthreads();
-    // each row's segment partials in order, the bias, one rounding
+    // each row's segment partials in order, the bias, one rounding; out is
+    // [m, rows of its tensor]
     const void* bias_a = pick(g.bias, ia);
     const void* bias_b = pick(g.bias, ib);
     void* out_a = pick(g.out, ia);
     void* out_b = pick(g.out, ib);
-    for (uint32_t t = threadIdx.x; t < nrows; t += kSipThreads) {
+    uint32_t rows_b = g.row0[1] - g.row0[0];
+#pragma unroll
+    for (int k = 1; k < kGroupMax; ++k) rows_b = ib == (uint32_t)k ? g.row0[k + 1] - g.row0[k] : rows_b;
+    const uint32_t rows_a = row_b - row_a;
+    for (uint32_t i = threadIdx.x; i < nrows * sh.m; i += kSipThreads) {
+        const uint32_t m = i / nrows, t = i - m * nrows;
         float sum = 0.0f;
-        for (uint32_t k = 0; k < sh.segs; ++k) sum += red[t * sh.segs + k];
+        for (uint32_t k = 0; k < sh.segs; ++k) sum += red[(t * sh.segs + k) * M + m];
         const bool in_b = t >= split;
         const uint32_t row = in_b ? t - split : lrow_a + t;
         const void* bias = in_b ? bias_b : bias_a;
         if (bias) sum += load_elem(bias, sh.bias_dtype, row);
-        store_elem(in_b ? out_b : out_a, sh.out_dtype, row, sum);
+        store_elem(in_b ? out_b : out_a, sh.out_dtype, (uint64_t)m * (in_b ? rows_b : rows_a) + row, sum);
     }
 }
 
@@ -822,16 +878,29 @@ int cu_count() {
 
 // Whether the sip kernel takes tensor t with this activation.
 bool sip_eligible(const dmx_radix_tensor* t, const void* x, int x_dtype, uint32_t m) {
-    return g_policy.load() == DMX_POLICY_AUTO && m == 1 && x_dtype == DMX_BF16 && is_sip(t) && t->block_size == 1024 &&
+    return g_policy.load() == DMX_POLICY_AUTO && m >= 1 && m <= 8 && x_dtype == DMX_BF16 && is_sip(t) &&
+           t->block_size == 1024 &&
            t->cols % 1024 == 0 && (reinterpret_cast<uintptr_t>(x) & 15u) == 0;
 }
 
 // One launch of the sip kernel over n tensors of equal cols (already
 // checked). Returns 2 when the group cannot run as one launch (a row tile
 // taller than a tensor, or tables past the LDS), having launched nothing.
-int launch_sip(const dmx_radix_tensor* const* ts, uint32_t n, const void* x, const void* const* bias, int bias_dtype,
-               void* const* out, int out_dtype, hipStream_t stream, char* err, size_t errn) {
-    if (n < 1 || n > (uint32_t)kGroupMax) return 2;
+typedef void (*SipKernel)(const SipGroup, const uint16_t*, const SipShape);
+
+// k_gemv_sip<two, M> for M = 1, 2, 4, 8 (index 0..3)
+SipKernel sip_kernel(bool two, int mi) {
+    static const SipKernel table[2][4] = {
+        {k_gemv_sip<false, 1>, k_gemv_sip<false, 2>, k_gemv_sip<false, 4>, k_gemv_sip<false, 8>},
+        {k_gemv_sip<true, 1>, k_gemv_sip<true, 2>, k_gemv_sip<true, 4>, k_gemv_sip<true, 8>}};
+    return table[two ? 1 : 0][mi];
+}
+
+int launch_sip(const dmx_radix_tensor* const* ts, uint32_t n, const void* x, uint32_t m, const void* const* bias,
+               int bias_dtype, void* const* out, int out_dtype, hipStream_t stream, char* err, size_t errn) {
+    if (n < 1 || n > (uint32_t)kGroupMax || m < 1 || m > 8) return 2;
+    const int mi = m == 1 ? 0 : m == 2 ? 1 : m <= 4 ? 2 : 3;
+    const uint32_t M = 1u << mi;
     SipGroup g;
     SipShape sh;
     uint64_t total = 0;
@@ -856,51 +925,57 @@ int launch_sip(const dmx_radix_tensor* const* ts, uint32_t n, const void* x, con
     sh.cols = ts[0]->cols;
     sh.nb = sh.cols / 1024;
     sh.n = n;
+    sh.m = m;
     sh.bias_dtype = bias_dtype;
     sh.out_dtype = out_dtype;
-    // one workgroup per slot (two per CU), T rows each; S segments per row
-    // so that the T * S units deal evenly to the waves
-    uint32_t grid = std::min<uint32_t>(sh.rows, (uint32_t)cu_count() * 2);
-    sh.rows_per_wg = (sh.rows + grid - 1) / grid;
-    if (sh.rows_per_wg > min_rows) return 2;
-    grid = (sh.rows + sh.rows_per_wg - 1) / sh.rows_per_wg;
-    // S: the fewest block-times per workgroup, a unit's closing wave sum
-    // costing about a quarter of a block
-    double best = 1e30;
-    sh.segs = 1;
-    for (uint32_t s = 1; s <= std::min<uint32_t>(sh.nb, kSipWaves); ++s) {
-        if (sh.nb % s) continue;
-        const double rounds = std::ceil((double)sh.rows_per_wg * s / kSipWaves);
-        const double cost = rounds * ((double)(sh.nb / s) + 0.25);
-        if (cost < best - 1e-9) {
-            best = cost;
-            sh.segs = s;
-        }
-    }
-    sh.seg_blocks = sh.nb / sh.segs;
-    // a workgroup spans two tensors where a tensor starts inside its tile
-    bool two = false;
-    for (uint32_t i = 1; i < n; ++i) two |= g.row0[i] % sh.rows_per_wg != 0;
-    const size_t head = 2 * (size_t)sh.cols + (((size_t)sh.rows_per_wg * sh.segs * 4 + 15) & ~(size_t)15);
-    sh.tbl2_lds = two ? (uint32_t)head : 0u;
-    const size_t lds = head + (two ? kTableBytes : 0);
+    // one workgroup per slot (two per CU where their LDS fits, else one), T
+    // rows each; S segments per row so that the T * S units deal evenly to
+    // the waves
     const size_t fixed = kTableBytes + kSelBytes;
-    if (lds + fixed > 160 * 1024) return 2;
+    uint32_t grid = 0;
+    size_t lds = 0;
+    bool two = false;
+    // (M = 8's registers allow one workgroup per CU)
+    for (uint32_t per_cu = M == 8 ? 1 : 2; per_cu >= 1; --per_cu) {
+        grid = std::min<uint32_t>(sh.rows, (uint32_t)cu_count() * per_cu);
+        sh.rows_per_wg = (sh.rows + grid - 1) / grid;
+        if (sh.rows_per_wg > min_rows) return 2;
+        grid = (sh.rows + sh.rows_per_wg - 1) / sh.rows_per_wg;
+        // S: the fewest block-times per workgroup, each of a unit's closing
+        // wave sums (one per activation row) costing about a quarter of a block
+        double best = 1e30;
+        sh.segs = 1;
+        for (uint32_t s = 1; s <= std::min<uint32_t>(sh.nb, kSipWaves); ++s) {
+            if (sh.nb % s) continue;
+            const double rounds = std::ceil((double)sh.rows_per_wg * s / kSipWaves);
+            const double cost = rounds * ((double)(sh.nb / s) + 0.25 * M);
+            if (cost < best - 1e-9) {
+                best = cost;
+                sh.segs = s;
+            }
+        }
+        sh.seg_blocks = sh.nb / sh.segs;
+        // a workgroup spans two tensors where a tensor starts inside its tile
+        two = false;
+        for (uint32_t i = 1; i < n; ++i) two |= g.row0[i] % sh.rows_per_wg != 0;
+        const size_t head = 2 * (size_t)M * sh.cols + (((size_t)sh.rows_per_wg * sh.segs * M * 4 + 15) & ~(size_t)15);
+        sh.tbl2_lds = two ? (uint32_t)head : 0u;
+        lds = head + (two ? kTableBytes : 0);
+        if ((lds + fixed) * per_cu <= 160 * 1024) break;
+        if (per_cu == 1) return 2;
+    }
     static std::atomic<size_t> lds_opted{64 * 1024 - fixed};
     if (lds > lds_opted.load()) {
-        for (const void* k : {reinterpret_cast<const void*>(k_gemv_sip<false>),
-                              reinterpret_cast<const void*>(k_gemv_sip<true>)}) {
-            hipError_t e = hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-            if (e != hipSuccess) return fail_hip(err, errn, "sip kernel LDS opt-in", e);
-        }
+        for (int t = 0; t < 2; ++t)
+            for (int i = 0; i < 4; ++i) {
+                hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(sip_kernel(t, i)),
+                                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+                if (e != hipSuccess) return fail_hip(err, errn, "sip kernel LDS opt-in", e);
+            }
         lds_opted.store(lds);
     }
-    if (two)
-        hipLaunchKernelGGL(k_gemv_sip<true>, dim3(grid), dim3(kSipThreads), lds, stream, g,
-                           static_cast<const uint16_t*>(x), sh);
-    else
-        hipLaunchKernelGGL(k_gemv_sip<false>, dim3(grid), dim3(kSipThreads), lds, stream, g,
-                           static_cast<const uint16_t*>(x), sh);
+    hipLaunchKernelGGL(sip_kernel(two, mi), dim3(grid), dim3(kSipThreads), lds, stream, g,
+                       static_cast<const uint16_t*>(x), sh);
     return launch_check(err, errn, "sip gemv launch");
 }
 
@@ -924,7 +999,7 @@ int check_gemv_args(const void* x, int x_dtype, uint32_t m, const void* bias, in
 int gemv_one(const dmx_radix_tensor* t, const Desc& d, const void* x, int x_dtype, uint32_t m, const void* bias,
              int bias_dtype, void* out, int out_dtype, hipStream_t s, char* err, size_t errn) {
     if (sip_eligible(t, x, x_dtype, m)) {
-        const int rc = launch_sip(&t, 1, x, &bias, bias_dtype, &out, out_dtype, s, err, errn);
+        const int rc = launch_sip(&t, 1, x, m, &bias, bias_dtype, &out, out_dtype, s, err, errn);
         if (rc != 2) return rc;
     }
     switch (m) {
@@ -998,7 +1073,7 @@ extern "C" int dmx_radix_gemv_group(const dmx_radix_tensor* const* tensors, uint
     }
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (one_launch) {
-        const int rc = launch_sip(tensors, n, x, bias, bias_dtype, out, out_dtype, s, err, errn);
+        const int rc = launch_sip(tensors, n, x, m, bias, bias_dtype, out, out_dtype, s, err, errn);
         if (rc != 2) return rc;
     }
     for (uint32_t i = 0; i < n; ++i) {

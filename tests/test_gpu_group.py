@@ -34,33 +34,33 @@ def _check(y, xf, bits, what):
 
 @pytest.mark.parametrize("rows", [(4096, 1024, 1024), (12288, 12288), (1000, 37, 2000), (5, 7), (300, 301, 302, 303),
                                   (2048,)])
-@pytest.mark.parametrize("C", [4096, 2048])
-def test_group_matches_the_oracle(cuda, rows, C):
+@pytest.mark.parametrize("C,M", [(4096, 1), (2048, 1), (4096, 4), (2048, 3), (1024, 8)])
+def test_group_matches_the_oracle(cuda, rows, C, M):
     import torch
 
     from drinkme_amd import radix_ops, swap
 
-    rng = np.random.default_rng(zlib.crc32(repr((rows, C)).encode()))
+    rng = np.random.default_rng(zlib.crc32(repr((rows, C, M)).encode()))
     kinds = ("tight", "spread", "escapes", "tight")
     bits = [_bits(rng, (r, C), kinds[i % 4]) for i, r in enumerate(rows)]
     rts = [swap.to_device_radix(oracle_dict(b, "sip"), cuda) for b in bits]
     assert len({tuple(rt["rx_palette_np"]) for rt in rts}) > 1 or len(rts) == 1
-    xb = O.f32_to_bf16_bits(rng.standard_normal((1, C)).astype(np.float32))
+    xb = O.f32_to_bf16_bits(rng.standard_normal((M, C)).astype(np.float32))
     x = bf16_tensor(xb, cuda)
     xf = O.bf16_bits_to_f32(xb)
-    print(f"case group rows={rows} C={C}", flush=True)
-    ys = radix_ops.gemv_group(rts, x[0], None, torch.float32)
+    print(f"case group rows={rows} C={C} M={M}", flush=True)
+    ys = radix_ops.gemv_group(rts, x, None, torch.float32)
     for i, (y, b) in enumerate(zip(ys, bits)):
         _check(y.cpu().numpy(), xf, b, f"group {rows} tensor {i}")
     # biases (one missing), bf16 out: the epilogue rounds the fp32 sum once
     biases = [None if i == 1 else bf16_tensor(O.f32_to_bf16_bits(rng.standard_normal(r).astype(np.float32)), cuda)
               for i, r in enumerate(rows)]
-    fused = radix_ops.gemv_group(rts, x[0], biases, torch.bfloat16)
+    fused = radix_ops.gemv_group(rts, x, biases, torch.bfloat16)
     for i, (f, y) in enumerate(zip(fused, ys)):
         want = y if biases[i] is None else y + biases[i].float()
         assert torch.equal(f, want.to(torch.bfloat16)), f"group {rows} tensor {i}: fused epilogue"
     # twice more: deterministic
-    again = radix_ops.gemv_group(rts, x[0], None, torch.float32)
+    again = radix_ops.gemv_group(rts, x, None, torch.float32)
     assert all(torch.equal(a, b) for a, b in zip(again, ys))
 
 
