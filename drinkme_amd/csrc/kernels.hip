@@ -337,6 +337,7 @@ struct SipGroup {
     const uint32_t* data[kGroupMax];
     const uint32_t* offsets[kGroupMax];
     const uint32_t* palette[kGroupMax];
+    const uint16_t* schedule[kGroupMax];  // gulp: the per-block tier stream lengths
     const void* bias[kGroupMax];
     void* out[kGroupMax];
     uint32_t row0[kGroupMax + 1];  // row0[n] = the group's row count
@@ -794,6 +795,428 @@ __global__ __launch_bounds__(kSipThreads, M == 8 ? 3 : 6) void k_gemv_sip(const 
     }
 }
 
+// ------------------------------------------------- gulp, M rows, whole blocks --
+//
+// gulp (2, 2, 4, 8): per 1024-weight block the literal plane (256 words),
+// tier 0 (64 words of 2-bit codes: palette entries 0..2, code 3 escapes),
+// tier 1 (2-bit codes of the tier-0 escapes: entries 3..5), tier 2 (4-bit
+// codes of the tier-1 escapes: entries 6..20) and the terminal (the raw
+// exponents of the tier-2 escapes). The per-block schedule
+// (dmx_radix_prepare) gives tier 1's and tier 2's word counts, so every
+// stream's start is known when the block's loads are issued.
+//
+// The work split, load pipeline and products are the sip kernel's. Lane l
+// owns weights 16l .. 16l + 15; per group of four weights:
+//   tier 0  a 256-entry LDS table indexed by the four codes gives the
+//           exponents of the resolved weights and the escape mask m0;
+//   tier 1  the lane's tier-1 codes are a 32-bit window of the tier-1
+//           stream at bit 2 q0 (q0: the wave's exclusive prefix of tier-0
+//           escape counts), pulled from the lanes holding it (lane j holds
+//           tier-1 word j); a 4096-entry table indexed by (the group's next
+//           four codes, m0) gives the tier-1 exponents at the escaped
+//           positions and the tier-1 escape mask m1;
+//   tier 2  lane j resolves tier-1 escapes 2j and 2j + 1 of the block from
+//           the tier-2 word it loaded (and the terminal, for code 15) and
+//           writes their exponent bytes to the wave's LDS array; each lane
+//           reads the 8-byte window of that array at its first rank q1 and
+//           places the bytes with the selector table, as sip places its
+//           terminal bytes.
+// A block with more than 128 tier-1 escapes, or a lane with more than 8,
+// takes an exact lane-serial path that reads the streams from memory.
+
+constexpr uint32_t kGulpFixed = 256 + 64;  // literal plane + tier 0 words of a 1024-weight block
+constexpr uint32_t kGulpT0Bytes = 256 * 8;
+constexpr uint32_t kGulpX2Words = 40;     // per wave: 128 exponent bytes + a window's overhang
+
+struct GulpStage {
+    u32x4 lit;
+    uint32_t t0, t1, t2, term;
+    uint32_t start, end, sched;
+};
+
+// Per-lane byte offsets of a gulp block's loads: 16 literal bytes, tier-0
+// word l, tier-1 word l (from the tier-1 start), tier-2 word l / 4 (from the
+// tier-2 start) and terminal word l (from the terminal start).
+struct GulpLanes {
+    uint32_t lit, t0, t1, t2, term;
+};
+
+// The block's five loads through the workgroup's buffer resource (based at
+// its first block), untracked by the compiler as in sip_load; completed by
+// GULP_WAIT. Reads reach at most word 320 + 64 + 128 + 63 of the block,
+// inside block_word_bounds(1024)[1] = 768.
+__device__ __forceinline__ GulpStage gulp_load(i32x4 rsrc, uint32_t base, uint2 o, uint32_t sched,
+                                               const GulpLanes& ln) {
+    GulpStage s;
+    s.start = o.x;
+    s.end = o.y;
+    s.sched = sched;
+    // (a schedule byte past its stream's widest keeps every read in the pad)
+    const uint32_t w1 = min(sched & 0xFFu, 64u), w2 = min(sched >> 8, 128u);
+    const uint32_t soff = (o.x - base) * 4u;
+    const uint32_t soff2 = soff + 4u * (kGulpFixed + w1);
+    const uint32_t soff3 = soff2 + 4u * w2;
+    asm volatile(
+        "buffer_load_dword %0, %5, %10, %12 offen\n\t"
+        "buffer_load_dword %1, %6, %10, %11 offen\n\t"
+        "buffer_load_dword %2, %7, %10, %13 offen\n\t"
+        "buffer_load_dword %3, %8, %10, %13 offen\n\t"
+        "buffer_load_dwordx4 %4, %9, %10, %13 offen"
+        : "=&v"(s.term), "=&v"(s.t2), "=&v"(s.t1), "=&v"(s.t0), "=&v"(s.lit)
+        : "v"(ln.term), "v"(ln.t2), "v"(ln.t1), "v"(ln.t0), "v"(ln.lit), "s"(rsrc), "s"(soff2), "s"(soff3),
+          "s"(soff));
+    return s;
+}
+
+#define GULP_WAIT(N, S) \
+    asm volatile("s_waitcnt vmcnt(" #N ")" : "+v"(S.lit), "+v"(S.t0), "+v"(S.t1), "+v"(S.t2), "+v"(S.term))
+
+// Field i of width w of the little-endian stream at p, through the vector
+// memory path (the lane-serial fallback).
+__device__ __forceinline__ uint32_t gulp_field(const uint32_t* p, uint32_t i, uint32_t w) {
+    const uint32_t bit = i * w;
+    const uint64_t pair = (uint64_t)p[(bit >> 5) + 1] << 32 | p[bit >> 5];
+    return (uint32_t)(pair >> (bit & 31u)) & ((1u << w) - 1u);
+}
+
+// Builds the gulp tables of a palette (6 words: tier 0, tier 1, tier 2 x 4,
+// each entry list padded with a zero byte that the escape code reads):
+//   t0tab[c0 | c1 << 2 | c2 << 4 | c3 << 6]: E(c0) << 7 | E(c1) << 23 |
+//       m0 << 3 | 2 popcount(m0) << 15, and E(c2) << 7 | E(c3) << 23;
+//   t1tab[codes << 4 | m0]: the same for tier 1, the four codes taken in
+//       order by the escaped positions of m0 (others 0), with m1 (the
+//       positions whose tier-1 code escapes) << 3 | popcount(m1) << 15;
+//   pal2[c]: tier 2's bytes.
+__device__ __forceinline__ void gulp_tables(uint2* t0tab, uint2* t1tab, uint8_t* pal2, const uint32_t* palette) {
+    const const_u32_ptr pw = (const_u32_ptr)palette;
+    const uint32_t p0 = pw[0], p1 = pw[1];
+    for (uint32_t i = threadIdx.x; i < 256; i += kSipThreads) {
+        uint32_t e[4], m = 0;
+        for (uint32_t k = 0; k < 4; ++k) {
+            const uint32_t c = (i >> (2 * k)) & 3u;
+            e[k] = (p0 >> (8 * c)) & 0xFFu;
+            m |= (c == 3u) << k;
+        }
+        t0tab[i] = make_uint2((e[0] << 7) | (e[1] << 23) | (m << 3) | ((2u * __builtin_popcount(m)) << 15),
+                              (e[2] << 7) | (e[3] << 23));
+    }
+    for (uint32_t i = threadIdx.x; i < 4096; i += kSipThreads) {
+        const uint32_t m0 = i & 15u, codes = i >> 4;
+        uint32_t e[4], m1 = 0, r = 0;
+        for (uint32_t k = 0; k < 4; ++k) {
+            e[k] = 0;
+            if ((m0 >> k) & 1u) {
+                const uint32_t c = (codes >> (2 * r++)) & 3u;
+                e[k] = (p1 >> (8 * c)) & 0xFFu;
+                m1 |= (c == 3u) << k;
+            }
+        }
+        t1tab[i] = make_uint2((e[0] << 7) | (e[1] << 23) | (m1 << 3) | ((uint32_t)__builtin_popcount(m1) << 15),
+                              (e[2] << 7) | (e[3] << 23));
+    }
+    if (threadIdx.x < 4) reinterpret_cast<uint32_t*>(pal2)[threadIdx.x] = pw[2 + threadIdx.x];
+}
+
+template <int M>
+__global__ __launch_bounds__(kSipThreads, M == 8 ? 3 : 6) void k_gemv_gulp(const SipGroup g, const uint16_t* __restrict__ x,
+                                                                        const SipShape sh) {
+    __shared__ uint2 t0tab[256];
+    __shared__ uint2 t1tab[4096];
+    __shared__ uint2 sel2[13 * 16];
+    __shared__ uint32_t pal2w[4];
+    __shared__ uint32_t x2_all[kSipWaves * kGulpX2Words];
+    extern __shared__ __align__(16) uint8_t lds_dyn[];
+    uint16_t* xs = reinterpret_cast<uint16_t*>(lds_dyn);
+    float* red = reinterpret_cast<float*>(lds_dyn + 2 * M * sh.cols);
+    const uint8_t* pal2 = reinterpret_cast<const uint8_t*>(pal2w);
+
+    const uint32_t wv = wave_id(), lane = lane_id();
+    const uint32_t r0 = blockIdx.x * sh.rows_per_wg;
+    const uint32_t nrows = min(sh.rows - r0, sh.rows_per_wg);
+    const uint32_t units = nrows * sh.segs;
+    // the workgroup's tensor (tiles never span two in this kernel)
+    uint32_t ia = 0;
+#pragma unroll
+    for (int i = 1; i < kGroupMax; ++i) ia += (uint32_t)i < sh.n && g.row0[i] <= r0;
+    uint32_t row_a = g.row0[0], row_n = g.row0[1];
+#pragma unroll
+    for (int k = 1; k < kGroupMax; ++k) {
+        row_a = ia == (uint32_t)k ? g.row0[k] : row_a;
+        row_n = ia == (uint32_t)k ? g.row0[k + 1] : row_n;
+    }
+    const uint32_t* data = pick(g.data, ia);
+    const uint32_t* offsets = pick(g.offsets, ia);
+    const uint32_t* sched = reinterpret_cast<const uint32_t*>(pick(g.schedule, ia));
+    const uint32_t lrow = r0 - row_a;
+    SipSpan sp;
+    sp.a_first = lrow * sh.nb;
+    sp.split_blocks = nrows * sh.nb;
+    uint32_t* x2 = x2_all + wv * kGulpX2Words;
+
+    // the activation rows, swizzled as in the sip kernel
+    const uint32_t xchunks = sh.cols / 8;
+    for (uint32_t i = threadIdx.x; i < M * xchunks; i += kSipThreads) {
+        const uint32_t m = i / xchunks, j = i - m * xchunks, q = j & 127u;
+        const uint32_t src = min(m, sh.m - 1) * xchunks + ((j & ~127u) | (q < 64u ? 2u * q : 2u * (q - 64u) + 1u));
+        __builtin_amdgcn_global_load_lds((glb_ptr)(reinterpret_cast<const uint4*>(x) + src),
+                                         (lds_ptr)(reinterpret_cast<uint4*>(xs) + (i - lane)), 16, 0, 0);
+    }
+
+    SipCursor p, c;
+    sip_start<false>(sh, p, wv, sp);
+    c = p;
+    const uint32_t base = ((const_u32_ptr)offsets)[sp.a_first];
+    const i32x4 rsrc = make_rsrc(data + base, 0x7FFFFFFFu);
+    GulpLanes ln;
+    ln.lit = 16 * lane;
+    ln.t0 = 4 * (256 + lane);
+    ln.t1 = 4 * (kGulpFixed + lane);
+    ln.t2 = 4 * (lane >> 2);
+    ln.term = 4 * lane;
+    uint32_t ns = 0;  // the schedule of the last next_offsets() block
+    auto next_offsets = [&]() {
+        const uint32_t blk = p.u < units ? p.blk : sp.a_first;
+        const uint2 o = sip_offsets(offsets, blk);
+        ns = (((const_u32_ptr)sched)[blk >> 1] >> ((blk & 1u) * 16)) & 0xFFFFu;
+        sip_next<false>(sh, p, sp);
+        return o;
+    };
+    const uint2 oA = next_offsets();
+    const uint32_t nA = ns;
+    const uint2 oB = next_offsets();
+    const uint32_t nB = ns;
+    uint2 oC = next_offsets();
+    uint32_t nC = ns;
+    GulpStage sA = gulp_load(rsrc, base, oA, nA, ln);
+    __builtin_amdgcn_sched_barrier(0);
+    GulpStage sB = gulp_load(rsrc, base, oB, nB, ln);
+    __builtin_amdgcn_sched_barrier(0);
+    GulpStage sC;
+
+    gulp_tables(t0tab, t1tab, reinterpret_cast<uint8_t*>(pal2w), pick(g.palette, ia));
+    for (uint32_t i = threadIdx.x; i < 13 * 16; i += kSipThreads) {
+        const uint32_t m = i & 15, o = i >> 4;
+        uint32_t b[4];
+        for (uint32_t k = 0, r = o; k < 4; ++k) b[k] = (m >> k) & 1 ? (r++ & 7) : 0x0Cu;
+        sel2[i] = make_uint2(b[0] | 0x0C00u | (b[1] << 16) | 0x0C000000u, b[2] | 0x0C00u | (b[3] << 16) | 0x0C000000u);
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+
+    const uint32_t keep = 0x807F807Fu;
+    const uint32_t* palg = pick(g.palette, ia);
+    float acc0 = 0.0f, acc1 = 0.0f;
+    float acc[M];
+#pragma unroll
+    for (int m = 0; m < M; ++m) acc[m] = 0.0f;
+
+    auto process = [&](const GulpStage& s0) {
+        const uint32_t w1 = min(s0.sched & 0xFFu, 64u), w2 = min(s0.sched >> 8, 128u);
+        const bool has_term = s0.end > s0.start + kGulpFixed + w1 + w2;
+        // tier 0
+        const uint32_t T0 = s0.t0;
+        uint2 E0 = t0tab[T0 & 0xFF];
+        uint2 E1 = t0tab[(T0 >> 8) & 0xFF];
+        uint2 E2 = t0tab[(T0 >> 16) & 0xFF];
+        uint2 E3 = t0tab[T0 >> 24];
+        const uint16_t* xb = xs + c.cb * 1024 + 8 * lane;
+        uint4 xa, xc;
+        if (M == 1) {
+            __builtin_memcpy(&xa, xb, 16);
+            __builtin_memcpy(&xc, xb + 512, 16);
+        }
+        // twice the tier-0 escapes of each group, and their prefix in the lane
+        const uint32_t h0 = (E0.x >> 15) & 15u, h1 = (E1.x >> 15) & 15u, h2 = (E2.x >> 15) & 15u;
+        const uint32_t o1 = h0, o2 = o1 + h1, o3 = o2 + h2, cnt1 = (o3 + ((E3.x >> 15) & 15u)) >> 1;
+        const uint32_t q0 = wave_scan_incl(cnt1) - cnt1;
+        // tier 1: the lane's codes, 2 bits each from bit 2 q0 of the stream
+        const int k1 = (int)((q0 >> 2) & ~3u);
+        const uint32_t v0 = __builtin_amdgcn_ds_bpermute(k1, s0.t1);
+        const uint32_t v1 = __builtin_amdgcn_ds_bpermute(k1 + 4, s0.t1);
+        const uint32_t W1 = __builtin_amdgcn_alignbit(v1, v0, (q0 & 15u) << 1);
+#define DMX_T1(E, off) t1tab[(__builtin_amdgcn_ubfe(W1, (off), 8) << 4) | ((E.x >> 3) & 15u)]
+        const uint2 P0 = DMX_T1(E0, 0u), P1 = DMX_T1(E1, o1), P2 = DMX_T1(E2, o2), P3 = DMX_T1(E3, o3);
+#undef DMX_T1
+        E0.x |= P0.x & 0x7F807F80u;
+        E0.y |= P0.y;
+        E1.x |= P1.x & 0x7F807F80u;
+        E1.y |= P1.y;
+        E2.x |= P2.x & 0x7F807F80u;
+        E2.y |= P2.y;
+        E3.x |= P3.x & 0x7F807F80u;
+        E3.y |= P3.y;
+        // tier 2: the lane's tier-1 escapes, their prefix over the wave
+        const uint32_t d0 = (P0.x >> 15) & 7u, d1 = (P1.x >> 15) & 7u, d2 = (P2.x >> 15) & 7u;
+        const uint32_t p1 = d0, p2 = p1 + d1, p3 = p2 + d2, cnt2 = p3 + ((P3.x >> 15) & 7u);
+        const uint32_t inc1 = wave_scan_incl(cnt2);
+        const uint32_t q1 = inc1 - cnt2;
+        const uint32_t n2 = __builtin_amdgcn_readlane(inc1, 63);
+        if (__builtin_expect(n2 > 128u || __builtin_amdgcn_ballot_w64(cnt2 > 8u) != 0, 0)) {
+            // exact lane-serial path over the streams in memory
+            const uint32_t* tp = data + s0.start;
+            const uint32_t* s1 = tp + kGulpFixed;
+            const uint32_t* s2 = s1 + w1;
+            const uint32_t* s3 = s2 + w2;
+            uint32_t c2 = 0;
+            for (uint32_t r = q0; r < q0 + cnt1; ++r) c2 += gulp_field(s1, r, 2) == 3u;
+            const uint32_t b1 = wave_scan_incl(c2) - c2;
+            uint32_t c3 = 0;
+            for (uint32_t r = b1; r < b1 + c2; ++r) c3 += gulp_field(s2, r, 4) == 15u;
+            const uint32_t b2 = wave_scan_incl(c3) - c3;
+            uint32_t ex[16];
+            uint32_t ra = q0, rb = b1, rc = b2;
+            const uint32_t pw0 = palg[0], pw1 = palg[1];
+            for (int i = 0; i < 16; ++i) {
+                const uint32_t code = (T0 >> (2 * i)) & 3u;
+                uint32_t e;
+                if (code < 3u) {
+                    e = (pw0 >> (8 * code)) & 0xFFu;
+                } else {
+                    const uint32_t c1 = gulp_field(s1, ra++, 2);
+                    if (c1 < 3u) {
+                        e = (pw1 >> (8 * c1)) & 0xFFu;
+                    } else {
+                        const uint32_t cc = gulp_field(s2, rb++, 4);
+                        if (cc < 15u)
+                            e = (palg[2 + (cc >> 2)] >> (8 * (cc & 3u))) & 0xFFu;
+                        else
+                            e = has_term ? gulp_field(s3, rc++, 8) : 0u;
+                    }
+                }
+                ex[i] = e;
+            }
+            E0 = make_uint2((ex[0] << 7) | (ex[1] << 23), (ex[2] << 7) | (ex[3] << 23));
+            E1 = make_uint2((ex[4] << 7) | (ex[5] << 23), (ex[6] << 7) | (ex[7] << 23));
+            E2 = make_uint2((ex[8] << 7) | (ex[9] << 23), (ex[10] << 7) | (ex[11] << 23));
+            E3 = make_uint2((ex[12] << 7) | (ex[13] << 23), (ex[14] << 7) | (ex[15] << 23));
+        } else {
+            // lane j resolves tier-1 escapes 2j, 2j + 1: their 4-bit codes sit in
+            // tier-2 word j / 4 (the one this lane loaded), code 15 escaping to
+            // the terminal
+            const uint32_t sh2 = (lane & 3u) << 3;
+            const uint32_t ca = (s0.t2 >> sh2) & 15u, cb = (s0.t2 >> (sh2 + 4)) & 15u;
+            uint32_t ea = pal2[ca], eb = pal2[cb];
+            const bool ta = 2 * lane < n2 && ca == 15u, tb = 2 * lane + 1 < n2 && cb == 15u;
+            if (__builtin_amdgcn_ballot_w64(ta || tb) != 0 && has_term) {
+                const uint32_t nt = (uint32_t)ta + (uint32_t)tb;
+                const uint32_t q3 = wave_scan_incl(nt) - nt;
+                // terminal byte r is byte r & 3 of word r >> 2, held by lane r >> 2
+                const uint32_t u0 = __builtin_amdgcn_ds_bpermute((int)((q3 >> 2) << 2), s0.term);
+                const uint32_t u1 = __builtin_amdgcn_ds_bpermute((int)(((q3 >> 2) + 1) << 2), s0.term);
+                const uint32_t tw = __builtin_amdgcn_alignbit(u1, u0, (q3 & 3u) << 3);
+                if (ta) ea = tw & 0xFFu;
+                if (tb) eb = ta ? (tw >> 8) & 0xFFu : tw & 0xFFu;
+            }
+            reinterpret_cast<uint16_t*>(x2)[lane] = (uint16_t)(ea | (eb << 8));
+            __builtin_amdgcn_wave_barrier();
+            // each lane's window of 8 exponent bytes from rank q1, placed by the
+            // selector of (its tier-1 escapes before the group, the group's m1)
+            const uint32_t kq = q1 >> 2;
+            const uint32_t y0 = x2[kq], y1 = x2[kq + 1], y2 = x2[kq + 2];
+            const uint32_t wlo = __builtin_amdgcn_alignbit(y1, y0, (q1 & 3u) << 3);
+            const uint32_t whi = __builtin_amdgcn_alignbit(y2, y1, (q1 & 3u) << 3);
+#define DMX_T2(E, P, off)                                                       \
+    {                                                                           \
+        const uint2 s = sel2[((off) << 4) | ((P.x >> 3) & 15u)];                \
+        E.x |= __builtin_amdgcn_perm(whi, wlo, s.x) << 7;                       \
+        E.y |= __builtin_amdgcn_perm(whi, wlo, s.y) << 7;                       \
+    }
+            DMX_T2(E0, P0, 0u)
+            DMX_T2(E1, P1, p1)
+            DMX_T2(E2, P2, p2)
+            DMX_T2(E3, P3, p3)
+#undef DMX_T2
+            __builtin_amdgcn_wave_barrier();
+        }
+        const uint32_t L0 = s0.lit.x, L1 = s0.lit.y, L2 = s0.lit.z, L3 = s0.lit.w;
+        uint32_t wp[8];
+        wp[0] = (__builtin_amdgcn_perm(L0, L0, 0x01010000) & keep) | (E0.x & ~keep);
+        wp[1] = (__builtin_amdgcn_perm(L0, L0, 0x03030202) & keep) | (E0.y & ~keep);
+        wp[2] = (__builtin_amdgcn_perm(L1, L1, 0x01010000) & keep) | (E1.x & ~keep);
+        wp[3] = (__builtin_amdgcn_perm(L1, L1, 0x03030202) & keep) | (E1.y & ~keep);
+        wp[4] = (__builtin_amdgcn_perm(L2, L2, 0x01010000) & keep) | (E2.x & ~keep);
+        wp[5] = (__builtin_amdgcn_perm(L2, L2, 0x03030202) & keep) | (E2.y & ~keep);
+        wp[6] = (__builtin_amdgcn_perm(L3, L3, 0x01010000) & keep) | (E3.x & ~keep);
+        wp[7] = (__builtin_amdgcn_perm(L3, L3, 0x03030202) & keep) | (E3.y & ~keep);
+        if (M == 1) {
+            acc0 = dot2(wp[0], xa.x, acc0);
+            acc1 = dot2(wp[1], xa.y, acc1);
+            acc0 = dot2(wp[2], xa.z, acc0);
+            acc1 = dot2(wp[3], xa.w, acc1);
+            acc0 = dot2(wp[4], xc.x, acc0);
+            acc1 = dot2(wp[5], xc.y, acc1);
+            acc0 = dot2(wp[6], xc.z, acc0);
+            acc1 = dot2(wp[7], xc.w, acc1);
+        } else {
+#pragma unroll
+            for (int m = 0; m < M; ++m) {
+                uint4 ya, yc;
+                __builtin_memcpy(&ya, xb + m * sh.cols, 16);
+                __builtin_memcpy(&yc, xb + m * sh.cols + 512, 16);
+                float a = acc[m];
+                a = dot2(wp[0], ya.x, a);
+                a = dot2(wp[1], ya.y, a);
+                a = dot2(wp[2], ya.z, a);
+                a = dot2(wp[3], ya.w, a);
+                a = dot2(wp[4], yc.x, a);
+                a = dot2(wp[5], yc.y, a);
+                a = dot2(wp[6], yc.z, a);
+                acc[m] = dot2(wp[7], yc.w, a);
+            }
+        }
+        if (c.j + 1 == sh.seg_blocks) {
+            if (M == 1) {
+                const float s = wave_sum_dpp(acc0 + acc1);
+                if (lane == 0) red[c.u] = s;
+                acc0 = acc1 = 0.0f;
+            } else {
+#pragma unroll
+                for (int m = 0; m < M; ++m) {
+                    const float s = wave_sum_dpp(acc[m]);
+                    if (lane == 0) red[c.u * M + m] = s;
+                    acc[m] = 0.0f;
+                }
+            }
+        }
+        sip_next<false>(sh, c, sp);
+    };
+    const uint32_t my_units = wv < units ? (units - wv + kSipWaves - 1) / kSipWaves : 0;
+    const uint32_t items = my_units * sh.seg_blocks;
+    uint32_t k = 0;
+    for (; k + 3 <= items; k += 3) {
+        sC = gulp_load(rsrc, base, oC, nC, ln);
+        uint2 oN = next_offsets();
+        uint32_t nN = ns;
+        GULP_WAIT(10, sA);
+        process(sA);
+        sA = gulp_load(rsrc, base, oN, nN, ln);
+        oN = next_offsets();
+        nN = ns;
+        GULP_WAIT(10, sB);
+        process(sB);
+        sB = gulp_load(rsrc, base, oN, nN, ln);
+        oC = next_offsets();
+        nC = ns;
+        GULP_WAIT(10, sC);
+        process(sC);
+    }
+    GULP_WAIT(5, sA);
+    if (k < items) process(sA);
+    GULP_WAIT(0, sB);
+    if (k + 1 < items) process(sB);
+    __syncthreads();
+    const void* bias = pick(g.bias, ia);
+    void* out = pick(g.out, ia);
+    const uint32_t rows_t = row_n - row_a;
+    for (uint32_t i = threadIdx.x; i < nrows * sh.m; i += kSipThreads) {
+        const uint32_t m = i / nrows, t = i - m * nrows;
+        float sum = 0.0f;
+        for (uint32_t k = 0; k < sh.segs; ++k) sum += red[(t * sh.segs + k) * M + m];
+        if (bias) sum += load_elem(bias, sh.bias_dtype, lrow + t);
+        store_elem(out, sh.out_dtype, (uint64_t)m * rows_t + lrow + t, sum);
+    }
+}
+
 // ------------------------------------------------------------- host side --
 
 int fail(char* err, size_t n, const char* msg) {
@@ -910,6 +1333,7 @@ int launch_sip(const dmx_radix_tensor* const* ts, uint32_t n, const void* x, uin
         g.data[i] = t->data;
         g.offsets[i] = t->offsets;
         g.palette[i] = t->palette;
+        g.schedule[i] = t->schedule;
         g.bias[i] = bias ? bias[i < n ? i : n - 1] : nullptr;
         g.out[i] = out[i < n ? i : n - 1];
         g.row0[i] = (uint32_t)total;
@@ -979,6 +1403,94 @@ int launch_sip(const dmx_radix_tensor* const* ts, uint32_t n, const void* x, uin
     return launch_check(err, errn, "sip gemv launch");
 }
 
+bool is_gulp(const dmx_radix_tensor* t) {
+    return t->n_widths == 4 && t->widths[0] == 2 && t->widths[1] == 2 && t->widths[2] == 4 && t->widths[3] == 8;
+}
+
+bool gulp_eligible(const dmx_radix_tensor* t, const void* x, int x_dtype, uint32_t m) {
+    return g_policy.load() == DMX_POLICY_AUTO && m >= 1 && m <= 8 && x_dtype == DMX_BF16 && is_gulp(t) &&
+           t->block_size == 1024 && t->cols % 1024 == 0 && t->schedule &&
+           (reinterpret_cast<uintptr_t>(t->schedule) & 3u) == 0 && (reinterpret_cast<uintptr_t>(x) & 15u) == 0;
+}
+
+typedef void (*GulpKernel)(const SipGroup, const uint16_t*, const SipShape);
+
+GulpKernel gulp_kernel(int mi) {
+    static const GulpKernel table[4] = {k_gemv_gulp<1>, k_gemv_gulp<2>, k_gemv_gulp<4>, k_gemv_gulp<8>};
+    return table[mi];
+}
+
+// One launch of the gulp kernel over n tensors of equal cols (already
+// checked). Returns 2, having launched nothing, when it cannot take the
+// group: a workgroup tile would span two tensors, or the LDS does not fit.
+int launch_gulp(const dmx_radix_tensor* const* ts, uint32_t n, const void* x, uint32_t m, const void* const* bias,
+                int bias_dtype, void* const* out, int out_dtype, hipStream_t stream, char* err, size_t errn) {
+    if (n < 1 || n > (uint32_t)kGroupMax || m < 1 || m > 8) return 2;
+    const int mi = m == 1 ? 0 : m == 2 ? 1 : m <= 4 ? 2 : 3;
+    const uint32_t M = 1u << mi;
+    SipGroup g;
+    SipShape sh;
+    uint64_t total = 0;
+    for (uint32_t i = 0; i < (uint32_t)kGroupMax; ++i) {
+        const dmx_radix_tensor* t = ts[i < n ? i : n - 1];
+        g.data[i] = t->data;
+        g.offsets[i] = t->offsets;
+        g.palette[i] = t->palette;
+        g.schedule[i] = t->schedule;
+        g.bias[i] = bias ? bias[i < n ? i : n - 1] : nullptr;
+        g.out[i] = out[i < n ? i : n - 1];
+        g.row0[i] = (uint32_t)total;
+        if (i < n) total += t->rows;
+    }
+    if (total >= (1ull << 31)) return 2;
+    for (uint32_t i = n; i <= (uint32_t)kGroupMax; ++i) g.row0[i] = (uint32_t)total;
+    sh.rows = (uint32_t)total;
+    sh.cols = ts[0]->cols;
+    sh.nb = sh.cols / 1024;
+    sh.n = n;
+    sh.m = m;
+    sh.tbl2_lds = 0;
+    sh.bias_dtype = bias_dtype;
+    sh.out_dtype = out_dtype;
+    const size_t fixed = kGulpT0Bytes + kTableBytes + 13 * 16 * 8 + 16 + kSipWaves * kGulpX2Words * 4;
+    uint32_t grid = 0;
+    size_t lds = 0;
+    for (uint32_t per_cu = M == 8 ? 1 : 2; per_cu >= 1; --per_cu) {
+        grid = std::min<uint32_t>(sh.rows, (uint32_t)cu_count() * per_cu);
+        sh.rows_per_wg = (sh.rows + grid - 1) / grid;
+        grid = (sh.rows + sh.rows_per_wg - 1) / sh.rows_per_wg;
+        for (uint32_t i = 1; i < n; ++i)
+            if (g.row0[i] % sh.rows_per_wg) return 2;
+        double best = 1e30;
+        sh.segs = 1;
+        for (uint32_t s = 1; s <= std::min<uint32_t>(sh.nb, kSipWaves); ++s) {
+            if (sh.nb % s) continue;
+            const double rounds = std::ceil((double)sh.rows_per_wg * s / kSipWaves);
+            const double cost = rounds * ((double)(sh.nb / s) + 0.25 * M);
+            if (cost < best - 1e-9) {
+                best = cost;
+                sh.segs = s;
+            }
+        }
+        sh.seg_blocks = sh.nb / sh.segs;
+        lds = 2 * (size_t)M * sh.cols + (((size_t)sh.rows_per_wg * sh.segs * M * 4 + 15) & ~(size_t)15);
+        if ((lds + fixed) * per_cu <= 160 * 1024) break;
+        if (per_cu == 1) return 2;
+    }
+    static std::atomic<size_t> lds_opted{64 * 1024 - fixed};
+    if (lds > lds_opted.load()) {
+        for (int i = 0; i < 4; ++i) {
+            hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(gulp_kernel(i)),
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+            if (e != hipSuccess) return fail_hip(err, errn, "gulp kernel LDS opt-in", e);
+        }
+        lds_opted.store(lds);
+    }
+    hipLaunchKernelGGL(gulp_kernel(mi), dim3(grid), dim3(kSipThreads), lds, stream, g, static_cast<const uint16_t*>(x),
+                       sh);
+    return launch_check(err, errn, "gulp gemv launch");
+}
+
 template <int M>
 void launch_generic_m(const Desc& d, const void* x, int x_dtype, const void* bias, int bias_dtype, void* out,
                       int out_dtype, hipStream_t stream) {
@@ -1000,6 +1512,10 @@ int gemv_one(const dmx_radix_tensor* t, const Desc& d, const void* x, int x_dtyp
              int bias_dtype, void* out, int out_dtype, hipStream_t s, char* err, size_t errn) {
     if (sip_eligible(t, x, x_dtype, m)) {
         const int rc = launch_sip(&t, 1, x, m, &bias, bias_dtype, &out, out_dtype, s, err, errn);
+        if (rc != 2) return rc;
+    }
+    if (gulp_eligible(t, x, x_dtype, m)) {
+        const int rc = launch_gulp(&t, 1, x, m, &bias, bias_dtype, &out, out_dtype, s, err, errn);
         if (rc != 2) return rc;
     }
     switch (m) {
@@ -1061,19 +1577,24 @@ extern "C" int dmx_radix_gemv_group(const dmx_radix_tensor* const* tensors, uint
                                     int out_dtype, void* stream, char* err, size_t errn) {
     if (!tensors || !out || n == 0) return fail(err, errn, "empty tensor group");
     Desc d[kGroupMax];
-    bool one_launch = n <= (uint32_t)kGroupMax;
+    bool all_sip = n <= (uint32_t)kGroupMax, all_gulp = all_sip;
     for (uint32_t i = 0; i < n; ++i) {
         Desc di;
         if (check_tensor(tensors[i], di, err, errn)) return 1;
         if (tensors[i]->cols != tensors[0]->cols) return fail(err, errn, "a tensor group must share cols (one activation)");
         if (check_gemv_args(x, x_dtype, m, bias ? bias[i] : nullptr, bias_dtype, out[i], out_dtype, err, errn))
             return 1;
-        one_launch = one_launch && sip_eligible(tensors[i], x, x_dtype, m);
+        all_sip = all_sip && sip_eligible(tensors[i], x, x_dtype, m);
+        all_gulp = all_gulp && gulp_eligible(tensors[i], x, x_dtype, m);
         if (i < (uint32_t)kGroupMax) d[i] = di;
     }
     hipStream_t s = static_cast<hipStream_t>(stream);
-    if (one_launch) {
+    if (all_sip) {
         const int rc = launch_sip(tensors, n, x, m, bias, bias_dtype, out, out_dtype, s, err, errn);
+        if (rc != 2) return rc;
+    }
+    if (all_gulp) {
+        const int rc = launch_gulp(tensors, n, x, m, bias, bias_dtype, out, out_dtype, s, err, errn);
         if (rc != 2) return rc;
     }
     for (uint32_t i = 0; i < n; ++i) {

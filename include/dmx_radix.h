@@ -58,8 +58,10 @@ typedef struct dmx_radix_tensor {
                                  zero-padded to whole words, tiers concatenated
                                  (src/drinkme/codec/radix_pack.py:333-350) */
     const uint16_t* schedule; /* rx_schedule: one u16 per block for > 2 tiers, else NULL
-                                 (read by no kernel of this library; carried so the
-                                 descriptor is the runtime dict's) */
+                                 (dmx_radix_prepare writes it). The gulp kernel reads it
+                                 in aligned 4-byte words: 4-byte aligned, with room for
+                                 an even number of entries; without it gulp GEMVs run on
+                                 the generic kernel */
     uint64_t payload_words;   /* NW */
     uint64_t pad_words;       /* zero words after the payload */
     uint32_t rows;            /* R */

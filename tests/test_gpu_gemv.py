@@ -179,3 +179,66 @@ def test_sip_work_split(cuda, R, C):
     fused = radix_ops.gemv_fused(rt, x[0], bf16_tensor(bias_bits, cuda), torch.bfloat16)
     want = (torch.from_numpy(y).to(cuda) + bf16_tensor(bias_bits, cuda).float()).to(torch.bfloat16)
     assert torch.equal(fused.reshape(-1), want)
+
+
+def _gulp_bits(rng, kind, shape):
+    from drinkme_amd import synth
+
+    R, C = shape
+    if kind == "normal":
+        return synth.weight("gulp-test", 0, "w", R, C)
+    if kind == "t4":
+        return synth.weight("gulp-test", 0, "t4", R, C, synth.STUDENT_T4)
+    if kind == "spread":
+        return finite_bits(rng, shape, spread=True)
+    if kind == "dense-tier1":
+        # 12 equally likely exponents: half the weights escape tier 1 (more
+        # than 128 per block: the lane-serial path)
+        exps = rng.integers(100, 112, size=shape).astype(np.uint16)
+    elif kind == "terminal":
+        # 90% on three exponents, 5% on three more, 5% over 40 rare ones:
+        # about 50 tier-1 escapes per block (the windowed path), 25 of the
+        # rare exponents past tier 2 (about 3% of the weights in the terminal)
+        u = rng.random(shape)
+        exps = np.where(u < 0.9, rng.integers(120, 123, size=shape),
+                        np.where(u < 0.95, rng.integers(116, 119, size=shape),
+                                 rng.integers(60, 100, size=shape))).astype(np.uint16)
+    else:
+        # 70% on three exponents, 30% over 40 rare ones: about 280 tier-1
+        # escapes per block (the lane-serial path), 16% of the weights in
+        # the terminal
+        exps = np.where(rng.random(shape) < 0.7, rng.integers(120, 123, size=shape),
+                        rng.integers(60, 100, size=shape)).astype(np.uint16)
+    bits = (exps << 7) | rng.integers(0, 128, shape, dtype=np.uint16)
+    return bits | (rng.integers(0, 2, shape, dtype=np.uint16) << 15)
+
+
+@pytest.mark.parametrize("kind", ["normal", "t4", "spread", "terminal", "dense-tier1", "terminal-heavy"])
+@pytest.mark.parametrize("M", [1, 3, 8])
+def test_gulp_fast_path(cuda, kind, M):
+    """The gulp kernel (M = 1..8) across tier-1, tier-2 and terminal escape
+    densities, against the float64 bound and the generic kernel."""
+    import torch
+
+    from drinkme_amd import radix_ops, swap
+
+    rng = np.random.default_rng(zlib.crc32(repr((kind, M)).encode()))
+    shape = (300, 3072)
+    bits = _gulp_bits(rng, kind, shape)
+    if O.pack(bits, "gulp").raw:
+        pytest.skip("stored raw")
+    rt = swap.to_device_radix(oracle_dict(bits, "gulp"), cuda)
+    xb = O.f32_to_bf16_bits(rng.standard_normal((M, shape[1])).astype(np.float32))
+    x = bf16_tensor(xb, cuda)
+    print(f"case gulp fast {kind} M={M}", flush=True)
+    y = radix_ops.gemv_rows(rt, x, None, torch.float32).cpu().numpy()
+    _check_bound(y, O.bf16_bits_to_f32(xb), bits, f"gulp {kind} M={M}")
+    bias = bf16_tensor(O.f32_to_bf16_bits(rng.standard_normal(shape[0]).astype(np.float32)), cuda)
+    fused = radix_ops.gemv_rows(rt, x, bias, torch.bfloat16)
+    assert torch.equal(fused, (torch.from_numpy(y).to(cuda) + bias.float()).to(torch.bfloat16))
+    prev = radix_ops.set_policy("generic")
+    try:
+        yg = radix_ops.gemv_rows(rt, x, None, torch.float32).cpu().numpy()
+    finally:
+        radix_ops.set_policy(prev)
+    _check_bound(yg, O.bf16_bits_to_f32(xb), bits, f"gulp {kind} M={M} generic")
