@@ -7,9 +7,15 @@ Workloads (seeded synthetic weights, drinkme_amd/synth.py):
   qwen3-8b-step   (default) one Qwen3-8B decode step's compressed Linears:
                   36 layers x q/k/v/o/gate/up/down + lm_head = 253 GEMVs,
                   N(0, 0.02) weights packed at sip, M = 1, bf16 x ~ N(0, 1)
-  qwen3-8b-layer  one such layer (7 GEMVs)
+  qwen3-8b-layer  one such layer (7 GEMVs), four copies rotated
+  32b-layer       one layer of the 32B-class stack (hidden 5120: q 8192 x 5120,
+                  k/v 1024 x 5120, o 5120 x 8192, gate/up 25600 x 5120, down
+                  5120 x 25600), Student-t(4) weights scaled to std 0.02, two
+                  copies rotated
   linear-4096     one 4096 x 4096 tensor (rotated over 32 packed copies so
                   the 256 MB last-level cache cannot hold them)
+--profile sip | gulp | balanced packs the weights at that profile; --m sets
+the activation rows (1 = decode, 4 = the MTP verify rows).
 
 A step is one sweep over the workload's GEMVs, captured once as a HIP graph
 and replayed; inputs are resident in HBM before timing starts. The GEMVs
@@ -18,8 +24,9 @@ grouped launch (dmx_radix_gemv_group), the others one launch each; the
 same sweep with one launch per GEMV is timed too (config.ungrouped).
 Reported:
   value       whole-sweep compressed-HBM GB/s = sum of algorithmic bytes /
-              step time, B = 4 NW + 4 (R NB + 1) + 7 + 2 C + 2 R per GEMV
-              (payload, directory, palette, bf16 x and out; not the pad)
+              step time, B = 4 NW + 4 (R NB + 1) + P + 2 M C + 2 M R per
+              GEMV (payload, directory, palette P = 7 sip / 21 gulp, bf16 x
+              and out; not the pad)
   roofline    the dominant kernel launch (the grouped gate/up GEMV of a
               layer, 2 x 12288 x 4096): its algorithmic bytes per launch /
               its average launch time, from HIP events around a graph of
@@ -56,18 +63,23 @@ def algorithmic_bytes(rt: dict, m: int = 1) -> int:
 
 
 def workload_items(name: str):
+    """(workload, layer, tensor, rows, cols, distribution) per GEMV."""
     from drinkme_amd import synth
 
+    N, T4 = synth.NORMAL, synth.STUDENT_T4
     if name == "qwen3-8b-step":
-        return [("qwen3-8b", layer, n, r, c) for layer, n, r, c in synth.qwen3_8b_step()]
+        return [("qwen3-8b", layer, n, r, c, N) for layer, n, r, c in synth.qwen3_8b_step()]
     if name == "qwen3-8b-layer":
-        return [("qwen3-8b", 0, n, r, c) for n, r, c in synth.QWEN3_8B_LAYER]
+        # four copies of the layer, so the sweep is not held by the 256 MB cache
+        return [("qwen3-8b", copy, n, r, c, N) for copy in range(4) for n, r, c in synth.QWEN3_8B_LAYER]
+    if name == "32b-layer":
+        return [("32b-class", copy, n, r, c, T4) for copy in range(2) for n, r, c in synth.CLASS_32B_LAYER]
     if name == "linear-4096":
-        return [("linear-4096", copy, "w", 4096, 4096) for copy in range(32)]
+        return [("linear-4096", copy, "w", 4096, 4096, N) for copy in range(32)]
     raise SystemExit(f"unknown workload {name!r}")
 
 
-def build_tensors(items, profile: str):
+def build_tensors(items, profile: str, m: int = 1):
     import numpy as np  # noqa: F401
 
     from drinkme_amd import radix_pack, swap, synth
@@ -75,13 +87,13 @@ def build_tensors(items, profile: str):
     tensors = []
     t0 = time.time()
     last = t0
-    for i, (wl, layer, name, R, C) in enumerate(items):
-        bits = synth.weight(wl, layer, name, R, C)
+    for i, (wl, layer, name, R, C, dist) in enumerate(items):
+        bits = synth.weight(wl, layer, name, R, C, dist)
         p = radix_pack.pack_array_radix(bits, profile)
         if p is None:
             raise SystemExit(f"{wl}/{layer}/{name}: radix would expand this tensor")
         rt = swap.to_device_radix(p, "cuda")
-        tensors.append({"layer": layer, "name": name, "R": R, "C": C, "rt": rt, "bytes": algorithmic_bytes(rt),
+        tensors.append({"layer": layer, "name": name, "R": R, "C": C, "rt": rt, "bytes": algorithmic_bytes(rt, m),
                         "bf16_bytes": 2 * R * C, "bpw": p["bpw"]})
         if time.time() - last > 10 or i + 1 == len(items):
             last = time.time()
@@ -174,8 +186,9 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="qwen3-8b-step",
-                    choices=["qwen3-8b-step", "qwen3-8b-layer", "linear-4096"])
+                    choices=["qwen3-8b-step", "qwen3-8b-layer", "32b-layer", "linear-4096"])
     ap.add_argument("--profile", default="sip", choices=["sip", "gulp", "balanced"])
+    ap.add_argument("--m", type=int, default=1, choices=range(1, 9), help="activation rows (MTP verify: 4)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernel-only", action="store_true",
                     help="only the dominant kernel's graph (for counter passes)")
@@ -196,12 +209,12 @@ def main() -> int:
     if args.kernel_only:
         items = [it for it in items if it[2] in ("gate", "up")][:16] or items[:8]
     log(f"workload {args.workload}: {len(items)} GEMVs, profile {args.profile}")
-    tensors = build_tensors(items, args.profile)
+    tensors = build_tensors(items, args.profile, args.m)
     xs = {}
     for c in sorted({t["C"] for t in tensors}):
-        xb = synth.activation(args.workload, f"x{c}", 1, c)
+        xb = synth.activation(args.workload, f"x{c}", args.m, c)
         xs[c] = torch.from_numpy(xb.view("int16")).view(torch.bfloat16).cuda()
-    outs = [torch.empty((1, t["R"]), dtype=torch.bfloat16, device="cuda") for t in tensors]
+    outs = [torch.empty((args.m, t["R"]), dtype=torch.bfloat16, device="cuda") for t in tensors]
     descs = [radix_ops.descriptor(t["rt"]) for t in tensors]
 
     import ctypes as ct
@@ -232,14 +245,14 @@ def main() -> int:
 
     def launch_group(gi):
         n, tarr, oarr, C = garrs[gi]
-        st = lib.dmx_radix_gemv_group(tarr, n, xs[C].data_ptr(), _native.DMX_BF16, 1, None, 0, oarr,
+        st = lib.dmx_radix_gemv_group(tarr, n, xs[C].data_ptr(), _native.DMX_BF16, args.m, None, 0, oarr,
                                       _native.DMX_BF16, stream(), err, len(err))
         if st:
             raise RuntimeError(err.value.decode())
 
     def launch(i):
         t = tensors[i]
-        st = lib.dmx_radix_gemv(ct.byref(descs[i]), xs[t["C"]].data_ptr(), _native.DMX_BF16, 1, None, 0,
+        st = lib.dmx_radix_gemv(ct.byref(descs[i]), xs[t["C"]].data_ptr(), _native.DMX_BF16, args.m, None, 0,
                                 outs[i].data_ptr(), _native.DMX_BF16, stream(), err, len(err))
         if st:
             raise RuntimeError(err.value.decode())
@@ -253,11 +266,13 @@ def main() -> int:
             launch(i)
 
     # the dominant launch: a layer's grouped gate/up (48% of the step's
-    # weights; down is 24%, lm_head 8%); else the largest launch
+    # weights; down is 24%, lm_head 8%), else the largest launch; timed over
+    # every launch of the same tensors' shapes in the sweep
     gbytes = [sum(tensors[i]["bytes"] for i in grp) for grp in groups]
-    dom = [gi for gi, grp in enumerate(groups) if sorted(tensors[i]["name"] for i in grp) == ["gate", "up"]]
-    if not dom:
-        dom = [gbytes.index(max(gbytes))]
+    sig = [tuple((tensors[i]["name"], tensors[i]["R"], tensors[i]["C"]) for i in grp) for grp in groups]
+    pick = next((gi for gi, grp in enumerate(groups) if sorted(tensors[i]["name"] for i in grp) == ["gate", "up"]),
+                gbytes.index(max(gbytes)))
+    dom = [gi for gi in range(len(groups)) if sig[gi] == sig[pick]]
     dom_shape = " + ".join(f"{tensors[i]['R']}x{tensors[i]['C']}" for i in groups[dom[0]])
 
     def dominant():
@@ -289,7 +304,7 @@ def main() -> int:
         f"{total_bytes / (ms_u * 1e-3) / 1e9:.0f} GB/s compressed")
     traffic = None
     tf = os.path.join(ROOT, "profiles", "traffic.json")
-    key = f"k_gemv_sip {dom_shape} {args.profile} M=1"
+    key = f"k_gemv_{args.profile} {dom_shape} {args.profile} M={args.m}"
     if os.path.exists(tf):
         traffic = json.load(open(tf)).get(key, {}).get("hbm_bytes_per_launch")
     cpu = None
@@ -299,7 +314,8 @@ def main() -> int:
         log(f"cpu baseline: {cpu['value']:.2f} GB/s ({cpu['ms_per_step']:.0f} ms per step, {cpu['cores']} threads)")
     out = {
         "metric": "compressed-HBM GB/s of the Qwen3-8B decode-step GEMV sweep (sip, M=1)"
-        if args.workload == "qwen3-8b-step" else f"compressed-HBM GB/s ({args.workload}, {args.profile}, M=1)",
+        if (args.workload, args.profile, args.m) == ("qwen3-8b-step", "sip", 1)
+        else f"compressed-HBM GB/s ({args.workload}, {args.profile}, M={args.m})",
         "value": round(value, 1),
         "unit": "GB/s",
         "n_gpus": 1,
@@ -312,7 +328,7 @@ def main() -> int:
         "dtype": "bf16",
         "data": "synthetic",
         "config": {
-            "workload": args.workload, "profile": args.profile, "m": 1, "gemvs": len(tensors),
+            "workload": args.workload, "profile": args.profile, "m": args.m, "gemvs": len(tensors),
             "weights": sum(t["R"] * t["C"] for t in tensors), "compressed_bytes": total_bytes,
             "bpw": round(8 * total_bytes / sum(t["R"] * t["C"] for t in tensors), 4),
             "us_per_sweep": round(ms * 1e3, 2), "pct_of_hbm_peak": round(100 * value / PEAK_GBPS, 2),
@@ -326,7 +342,8 @@ def main() -> int:
         "roofline": {
             "bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBPS, "unit": "GB/s",
             "frac": round(achieved / PEAK_GBPS, 4), "traffic": traffic,
-            "kernel": "k_gemv_sip", "shape": dom_shape,
+            "kernel": {"sip": "k_gemv_sip", "gulp": "k_gemv_gulp"}.get(args.profile, "k_gemv_generic"),
+            "shape": dom_shape,
             "bytes_per_launch": round(dom_bytes), "us_per_launch": round(dom_us, 3),
             "launches_timed": len(dom),
         },
