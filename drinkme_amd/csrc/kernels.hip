@@ -347,8 +347,13 @@ struct SipShape {
     uint32_t rows, cols, nb;  // rows of the whole group
     uint32_t n;               // tensors in the group
     uint32_t rows_per_wg;     // T
-    uint32_t segs;            // S
+    uint32_t segs;            // S (segments per row) = phases * psegs
     uint32_t seg_blocks;      // L = NB / S
+    uint32_t phases;          // P: column phases (1 = every activation column resident in LDS)
+    uint32_t phase_blocks;    // K = NB / P column blocks of activations in LDS at a time
+    uint32_t psegs;           // segments per phase
+    uint32_t phase_units;     // T * psegs units per phase
+    uint32_t dp, dr, ds;      // a wave's step of W units in a full tile: phases, rows, segments
     uint32_t tbl2_lds;        // dynamic-LDS byte offset of the second table; 0 = no workgroup spans two tensors
     uint32_t m;               // activation rows (<= the kernel's M; rows past m are padding)
     int bias_dtype, out_dtype;
@@ -434,11 +439,13 @@ __device__ __forceinline__ SipStage sip_load(i32x4 rsrc, uint32_t base, uint2 o,
 // reads them before the wait.
 #define SIP_WAIT(N, S) asm volatile("s_waitcnt vmcnt(" #N ")" : "+v"(S.lit), "+v"(S.t0), "+v"(S.term))
 
-// A wave's place in its work: unit u, block j of the unit, the block's index
-// in its tensor's directory, its column block, and which of the workgroup's
-// tensors it belongs to.
+// A wave's place in its work: block j of the unit, the block's index in its
+// tensor's directory, its column block among the resident activation
+// columns, and which of the workgroup's tensors it belongs to.
 struct SipCursor {
-    uint32_t u, j, blk, cb, t;
+    uint32_t j, blk, cb, t;
+    uint32_t p, r, sp;  // the unit: column phase, row of the workgroup, segment within the phase
+    uint32_t slot;      // the unit's row partial: row * S + segment
 };
 
 // The workgroup's blocks in row-major order: [0, split_blocks) are its
@@ -448,23 +455,101 @@ struct SipSpan {
     uint32_t a_first, split_blocks;
 };
 
+// A wave's walk over its units u = wave, wave + W, ... of the workgroup's
+// units, phase-major: unit (p, r, sp) covers row r's column blocks
+// [(p psegs + sp) L, + L). nrows rows; each phase holds nrows * psegs
+// units. The walk steps by W units with additions only (dp phases, dr
+// rows, ds segments); the divisions happen once per wave.
+struct SipWalk {
+    uint32_t nrows, dp, dr, ds;
+};
+
+__device__ __forceinline__ SipWalk sip_walk(const SipShape& sh, uint32_t nrows) {
+    SipWalk w;
+    w.nrows = nrows;
+    if (nrows == sh.rows_per_wg) {  // every tile but perhaps the last: the host's step
+        w.dp = sh.dp;
+        w.dr = sh.dr;
+        w.ds = sh.ds;
+    } else {
+        const uint32_t pu = nrows * sh.psegs, rem = kSipWaves % pu;
+        w.dp = kSipWaves / pu;
+        w.dr = rem / sh.psegs;
+        w.ds = rem - w.dr * sh.psegs;
+    }
+    return w;
+}
+
+// Sets the block fields of the cursor's unit.
 template <bool TWO>
-__device__ __forceinline__ void sip_start(const SipShape& sh, SipCursor& c, uint32_t u, const SipSpan& sp) {
-    c.u = u;
+__device__ __forceinline__ void sip_unit(const SipShape& sh, SipCursor& c, const SipSpan& sp) {
     c.j = 0;
-    const uint32_t wb = u * sh.seg_blocks;
-    c.cb = (u % sh.segs) * sh.seg_blocks;
+    const uint32_t seg = c.p * sh.psegs + c.sp;
+    c.slot = c.r * sh.segs + seg;
+    const uint32_t wb = c.r * sh.nb + seg * sh.seg_blocks;
+    c.cb = c.sp * sh.seg_blocks;
     c.t = TWO && wb >= sp.split_blocks;
     c.blk = c.t ? wb - sp.split_blocks : sp.a_first + wb;
 }
 
+// The cursor at unit u (< W: a wave's first unit), counted up from unit 0.
 template <bool TWO>
-__device__ __forceinline__ void sip_next(const SipShape& sh, SipCursor& c, const SipSpan& sp) {
-    if (++c.j == sh.seg_blocks)
-        sip_start<TWO>(sh, c, c.u + kSipWaves, sp);
-    else {
+__device__ __forceinline__ void sip_start(const SipShape& sh, SipCursor& c, uint32_t u, const SipWalk& w,
+                                          const SipSpan& sp) {
+    c.p = c.r = c.sp = 0;
+    for (uint32_t i = 0; i < u; ++i) {
+        if (++c.sp == sh.psegs) {
+            c.sp = 0;
+            if (++c.r == w.nrows) {
+                c.r = 0;
+                ++c.p;
+            }
+        }
+    }
+    sip_unit<TWO>(sh, c, sp);
+}
+
+template <bool TWO>
+__device__ __forceinline__ void sip_next(const SipShape& sh, SipCursor& c, const SipWalk& w, const SipSpan& sp) {
+    if (++c.j == sh.seg_blocks) {
+        c.p += w.dp;
+        c.r += w.dr;
+        c.sp += w.ds;
+        if (c.sp >= sh.psegs) {
+            c.sp -= sh.psegs;
+            ++c.r;
+        }
+        if (c.r >= w.nrows) {
+            c.r -= w.nrows;
+            ++c.p;
+        }
+        sip_unit<TWO>(sh, c, sp);
+    } else {
         ++c.blk;
         ++c.cb;
+    }
+}
+
+// Rows 0..M-1 of x, columns [phase K 1024, (phase + 1) K 1024), into LDS
+// by direct loads: row m at xs + m K 1024; within each 1024-column block,
+// 16-byte chunk q < 64 holds x[16q .. 16q + 7] and chunk 64 + q holds
+// x[16q + 8 .. 16q + 15], so a lane's two reads of its 16 activations each
+// cover 1 KB contiguously over the wave (no bank conflicts). A padding row
+// (m >= sh.m) repeats the last real row (its sums are never stored).
+template <int M, int THREADS>
+__device__ __forceinline__ void load_x_slice(const SipShape& sh, const uint16_t* __restrict__ x, uint16_t* xs,
+                                             uint32_t phase) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t row_chunks = sh.phase_blocks * 128u, xchunks = sh.cols / 8, first = phase * row_chunks;
+#pragma unroll
+    for (uint32_t m = 0; m < (uint32_t)M; ++m) {
+        const uint32_t src_row = min(m, sh.m - 1) * xchunks + first;
+        for (uint32_t j = threadIdx.x; j < row_chunks; j += THREADS) {
+            const uint32_t q = j & 127u, src = src_row + ((j & ~127u) | (q < 64u ? 2u * q : 2u * (q - 64u) + 1u));
+            __builtin_amdgcn_global_load_lds((glb_ptr)(reinterpret_cast<const uint4*>(x) + src),
+                                             (lds_ptr)(reinterpret_cast<uint4*>(xs) + m * row_chunks + (j - lane)),
+                                             16, 0, 0);
+        }
     }
 }
 
@@ -496,8 +581,11 @@ __device__ __forceinline__ void sip_table(uint2* tb, const uint32_t* palette) {
 // turn, so the decode is paid once per block whatever M is.
 // (M = 8 holds one workgroup per CU: its activation rows alone take 8 * 2 *
 // cols bytes of LDS, so it is given the registers of 3 waves per SIMD.)
-template <bool TWO, int M>
-__global__ __launch_bounds__(kSipThreads, M == 8 ? 3 : 6) void k_gemv_sip(const SipGroup g, const uint16_t* __restrict__ x,
+// PH: the activation columns come in phases (sh.phases > 1), for rows too
+// long for LDS; the other instantiations carry no phase code. (With M = 4
+// too, it keeps one workgroup per CU, for the registers.)
+template <bool TWO, int M, bool PH>
+__global__ __launch_bounds__(kSipThreads, (M == 8 || (PH && M == 4)) ? 3 : 6) void k_gemv_sip(const SipGroup g, const uint16_t* __restrict__ x,
                                                           const SipShape sh) {
     // fixed-size tables in static LDS (their addresses fold into the LDS
     // instructions' offsets); the activation, the row partials and a second
@@ -507,7 +595,7 @@ __global__ __launch_bounds__(kSipThreads, M == 8 ? 3 : 6) void k_gemv_sip(const 
     __shared__ uint2 sel2[13 * 16];
     extern __shared__ __align__(16) uint8_t lds_dyn[];
     uint16_t* xs = reinterpret_cast<uint16_t*>(lds_dyn);
-    float* red = reinterpret_cast<float*>(lds_dyn + 2 * M * sh.cols);
+    float* red = reinterpret_cast<float*>(lds_dyn + 2 * M * sh.phase_blocks * 1024);
     uint2* tbl2 = reinterpret_cast<uint2*>(lds_dyn + sh.tbl2_lds);
 
     const uint32_t wv = wave_id(), lane = lane_id();
@@ -537,26 +625,16 @@ __global__ __launch_bounds__(kSipThreads, M == 8 ? 3 : 6) void k_gemv_sip(const 
     sp.a_first = lrow_a * sh.nb;
     sp.split_blocks = split * sh.nb;
 
-    // the activation goes to LDS by direct loads (no registers staged), first
-    // in the queue: small and hot in L2; the barrier below waits for it.
-    // Within each 1024-column block, 16-byte chunk p < 64 of LDS holds
-    // x[16p .. 16p + 7] and chunk 64 + p holds x[16p + 8 .. 16p + 15], so a
-    // lane's two reads of its 16 activations each cover 1 KB contiguously
-    // over the wave (no bank conflicts).
-    // Row m of x sits at xs + m * cols; a padding row (m >= sh.m) repeats
-    // the last real row (its sums are never stored).
-    const uint32_t xchunks = sh.cols / 8;
-    for (uint32_t i = threadIdx.x; i < M * xchunks; i += kSipThreads) {
-        const uint32_t m = i / xchunks, j = i - m * xchunks, q = j & 127u;
-        const uint32_t src = min(m, sh.m - 1) * xchunks + ((j & ~127u) | (q < 64u ? 2u * q : 2u * (q - 64u) + 1u));
-        __builtin_amdgcn_global_load_lds((glb_ptr)(reinterpret_cast<const uint4*>(x) + src),
-                                         (lds_ptr)(reinterpret_cast<uint4*>(xs) + (i - lane)), 16, 0, 0);
-    }
+    // the activation (its first column phase) goes to LDS by direct loads
+    // (no registers staged), first in the queue: small and hot in L2; the
+    // barrier below waits for it
+    load_x_slice<M, kSipThreads>(sh, x, xs, 0);
 
     // the first two blocks' loads go out before the tables are built; a
     // cursor past the wave's work reads the workgroup's first block instead
     SipCursor p, c;
-    sip_start<TWO>(sh, p, wv, sp);
+    const SipWalk wk = sip_walk(sh, nrows);
+    sip_start<TWO>(sh, p, wv, wk, sp);
     c = p;
     // each tensor's payload window: from the workgroup's first block of it
     const uint32_t base_a = ((const_u32_ptr)offsets_a)[sp.a_first], base_b = ((const_u32_ptr)offsets_b)[0];
@@ -568,10 +646,10 @@ __global__ __launch_bounds__(kSipThreads, M == 8 ? 3 : 6) void k_gemv_sip(const 
     ln.term = 4 * (kSipFixed + lane);
     uint32_t nt = 0;  // the tensor of the last next_offsets() block
     auto next_offsets = [&]() {
-        const bool live = p.u < units;
+        const bool live = p.p < sh.phases;
         nt = TWO && live ? p.t : 0u;
         const uint2 o = sip_offsets(nt ? offsets_b : offsets_a, live ? p.blk : sp.a_first);
-        sip_next<TWO>(sh, p, sp);
+        sip_next<TWO>(sh, p, wk, sp);
         return o;
     };
     auto load = [&](uint2 o, uint32_t t) {
@@ -618,7 +696,20 @@ __global__ __launch_bounds__(kSipThreads, M == 8 ? 3 : 6) void k_gemv_sip(const 
 #pragma unroll
     for (int m = 0; m < M; ++m) acc[m] = 0.0f;
     // one block of the wave's work, from its loaded stage
+    // column phases: every wave walks all of them in order (so the barriers
+    // match); a phase's activations replace the last one's once every wave
+    // is past it
+    uint32_t cur_phase = 0;
+    auto phase_advance = [&]() {
+        __syncthreads();
+        ++cur_phase;
+        load_x_slice<M, kSipThreads>(sh, x, xs, cur_phase);
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+    };
     auto process = [&](const SipStage& s0) {
+        if (PH)
+            while (cur_phase < c.p) phase_advance();
         const uint2* tb = TWO && s0.t ? tbl2 : tbl;
         const uint64_t v = ((uint64_t)s0.t0.y << 32 | s0.t0.x) >> ((lane & 1) * 16);
         const uint32_t lo = (uint32_t)v, hi = (uint32_t)(v >> 32);
@@ -714,8 +805,8 @@ __global__ __launch_bounds__(kSipThreads, M == 8 ? 3 : 6) void k_gemv_sip(const 
 #pragma unroll
             for (int m = 0; m < M; ++m) {
                 uint4 ya, yc;
-                __builtin_memcpy(&ya, xb + m * sh.cols, 16);
-                __builtin_memcpy(&yc, xb + m * sh.cols + 512, 16);
+                __builtin_memcpy(&ya, xb + m * sh.phase_blocks * 1024, 16);
+                __builtin_memcpy(&yc, xb + m * sh.phase_blocks * 1024 + 512, 16);
                 float a = acc[m];
                 a = dot2(wp[0], ya.x, a);
                 a = dot2(wp[1], ya.y, a);
@@ -731,18 +822,18 @@ __global__ __launch_bounds__(kSipThreads, M == 8 ? 3 : 6) void k_gemv_sip(const 
         if (c.j + 1 == sh.seg_blocks) {
             if (M == 1) {
                 const float s = wave_sum_dpp(acc0 + acc1);
-                if (lane == 0) red[c.u] = s;
+                if (lane == 0) red[c.slot] = s;
                 acc0 = acc1 = 0.0f;
             } else {
 #pragma unroll
                 for (int m = 0; m < M; ++m) {
                     const float s = wave_sum_dpp(acc[m]);
-                    if (lane == 0) red[c.u * M + m] = s;
+                    if (lane == 0) red[c.slot * M + m] = s;
                     acc[m] = 0.0f;
                 }
             }
         }
-        sip_next<TWO>(sh, c, sp);
+        sip_next<TWO>(sh, c, wk, sp);
     };
     // three stages rotate roles (no register copies); each step issues the
     // stage two blocks ahead, then completes the oldest (six loads newer);
@@ -772,6 +863,8 @@ __global__ __launch_bounds__(kSipThreads, M == 8 ? 3 : 6) void k_gemv_sip(const 
     if (k < items) process(sA);
     SIP_WAIT(0, sB);
     if (k + 1 < items) process(sB);
+    if (PH)
+        while (cur_phase + 1 < sh.phases) phase_advance();
     __syncthreads();
     // each row's segment partials in order, the bias, one rounding; out is
     // [m, rows of its tensor]
@@ -834,11 +927,12 @@ struct GulpStage {
     uint32_t start, end, sched;
 };
 
-// Per-lane byte offsets of a gulp block's loads: 16 literal bytes, tier-0
-// word l, tier-1 word l (from the tier-1 start), tier-2 word l / 4 (from the
-// tier-2 start) and terminal word l (from the terminal start).
+// Per-lane byte offsets of a gulp block's loads: 16 literal bytes (lit),
+// tier-0 word l and tier-1 word l (w: 4l, plus the streams' constant starts
+// as instruction offsets), tier-2 word l / 4 (t2, from the tier-2 start) and
+// terminal word l (w, from the terminal start).
 struct GulpLanes {
-    uint32_t lit, t0, t1, t2, term;
+    uint32_t lit, w, t2;
 };
 
 // The block's five loads through the workgroup's buffer resource (based at
@@ -857,14 +951,13 @@ __device__ __forceinline__ GulpStage gulp_load(i32x4 rsrc, uint32_t base, uint2 
     const uint32_t soff2 = soff + 4u * (kGulpFixed + w1);
     const uint32_t soff3 = soff2 + 4u * w2;
     asm volatile(
-        "buffer_load_dword %0, %5, %10, %12 offen\n\t"
-        "buffer_load_dword %1, %6, %10, %11 offen\n\t"
-        "buffer_load_dword %2, %7, %10, %13 offen\n\t"
-        "buffer_load_dword %3, %8, %10, %13 offen\n\t"
-        "buffer_load_dwordx4 %4, %9, %10, %13 offen"
+        "buffer_load_dword %0, %5, %8, %10 offen\n\t"
+        "buffer_load_dword %1, %6, %8, %9 offen\n\t"
+        "buffer_load_dword %2, %5, %8, %11 offen offset:1280\n\t"
+        "buffer_load_dword %3, %5, %8, %11 offen offset:1024\n\t"
+        "buffer_load_dwordx4 %4, %7, %8, %11 offen"
         : "=&v"(s.term), "=&v"(s.t2), "=&v"(s.t1), "=&v"(s.t0), "=&v"(s.lit)
-        : "v"(ln.term), "v"(ln.t2), "v"(ln.t1), "v"(ln.t0), "v"(ln.lit), "s"(rsrc), "s"(soff2), "s"(soff3),
-          "s"(soff));
+        : "v"(ln.w), "v"(ln.t2), "v"(ln.lit), "s"(rsrc), "s"(soff2), "s"(soff3), "s"(soff));
     return s;
 }
 
@@ -917,8 +1010,8 @@ __device__ __forceinline__ void gulp_tables(uint2* t0tab, uint2* t1tab, uint8_t*
     if (threadIdx.x < 4) reinterpret_cast<uint32_t*>(pal2)[threadIdx.x] = pw[2 + threadIdx.x];
 }
 
-template <int M>
-__global__ __launch_bounds__(kSipThreads, M == 8 ? 3 : 6) void k_gemv_gulp(const SipGroup g, const uint16_t* __restrict__ x,
+template <int M, bool PH>
+__global__ __launch_bounds__(kSipThreads, (M == 8 || (PH && M == 4)) ? 3 : 6) void k_gemv_gulp(const SipGroup g, const uint16_t* __restrict__ x,
                                                                         const SipShape sh) {
     __shared__ uint2 t0tab[256];
     __shared__ uint2 t1tab[4096];
@@ -927,7 +1020,7 @@ __global__ __launch_bounds__(kSipThreads, M == 8 ? 3 : 6) void k_gemv_gulp(const
     __shared__ uint32_t x2_all[kSipWaves * kGulpX2Words];
     extern __shared__ __align__(16) uint8_t lds_dyn[];
     uint16_t* xs = reinterpret_cast<uint16_t*>(lds_dyn);
-    float* red = reinterpret_cast<float*>(lds_dyn + 2 * M * sh.cols);
+    float* red = reinterpret_cast<float*>(lds_dyn + 2 * M * sh.phase_blocks * 1024);
     const uint8_t* pal2 = reinterpret_cast<const uint8_t*>(pal2w);
 
     const uint32_t wv = wave_id(), lane = lane_id();
@@ -953,32 +1046,25 @@ __global__ __launch_bounds__(kSipThreads, M == 8 ? 3 : 6) void k_gemv_gulp(const
     sp.split_blocks = nrows * sh.nb;
     uint32_t* x2 = x2_all + wv * kGulpX2Words;
 
-    // the activation rows, swizzled as in the sip kernel
-    const uint32_t xchunks = sh.cols / 8;
-    for (uint32_t i = threadIdx.x; i < M * xchunks; i += kSipThreads) {
-        const uint32_t m = i / xchunks, j = i - m * xchunks, q = j & 127u;
-        const uint32_t src = min(m, sh.m - 1) * xchunks + ((j & ~127u) | (q < 64u ? 2u * q : 2u * (q - 64u) + 1u));
-        __builtin_amdgcn_global_load_lds((glb_ptr)(reinterpret_cast<const uint4*>(x) + src),
-                                         (lds_ptr)(reinterpret_cast<uint4*>(xs) + (i - lane)), 16, 0, 0);
-    }
+    // the activation rows (first column phase), as in the sip kernel
+    load_x_slice<M, kSipThreads>(sh, x, xs, 0);
 
     SipCursor p, c;
-    sip_start<false>(sh, p, wv, sp);
+    const SipWalk wk = sip_walk(sh, nrows);
+    sip_start<false>(sh, p, wv, wk, sp);
     c = p;
     const uint32_t base = ((const_u32_ptr)offsets)[sp.a_first];
     const i32x4 rsrc = make_rsrc(data + base, 0x7FFFFFFFu);
     GulpLanes ln;
     ln.lit = 16 * lane;
-    ln.t0 = 4 * (256 + lane);
-    ln.t1 = 4 * (kGulpFixed + lane);
+    ln.w = 4 * lane;
     ln.t2 = 4 * (lane >> 2);
-    ln.term = 4 * lane;
     uint32_t ns = 0;  // the schedule of the last next_offsets() block
     auto next_offsets = [&]() {
-        const uint32_t blk = p.u < units ? p.blk : sp.a_first;
+        const uint32_t blk = p.p < sh.phases ? p.blk : sp.a_first;
         const uint2 o = sip_offsets(offsets, blk);
         ns = (((const_u32_ptr)sched)[blk >> 1] >> ((blk & 1u) * 16)) & 0xFFFFu;
-        sip_next<false>(sh, p, sp);
+        sip_next<false>(sh, p, wk, sp);
         return o;
     };
     const uint2 oA = next_offsets();
@@ -1010,7 +1096,20 @@ __global__ __launch_bounds__(kSipThreads, M == 8 ? 3 : 6) void k_gemv_gulp(const
 #pragma unroll
     for (int m = 0; m < M; ++m) acc[m] = 0.0f;
 
+    // column phases: every wave walks all of them in order (so the barriers
+    // match); a phase's activations replace the last one's once every wave
+    // is past it
+    uint32_t cur_phase = 0;
+    auto phase_advance = [&]() {
+        __syncthreads();
+        ++cur_phase;
+        load_x_slice<M, kSipThreads>(sh, x, xs, cur_phase);
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+    };
     auto process = [&](const GulpStage& s0) {
+        if (PH)
+            while (cur_phase < c.p) phase_advance();
         const uint32_t w1 = min(s0.sched & 0xFFu, 64u), w2 = min(s0.sched >> 8, 128u);
         const bool has_term = s0.end > s0.start + kGulpFixed + w1 + w2;
         // tier 0
@@ -1063,9 +1162,10 @@ __global__ __launch_bounds__(kSipThreads, M == 8 ? 3 : 6) void k_gemv_gulp(const
             uint32_t c3 = 0;
             for (uint32_t r = b1; r < b1 + c2; ++r) c3 += gulp_field(s2, r, 4) == 15u;
             const uint32_t b2 = wave_scan_incl(c3) - c3;
-            uint32_t ex[16];
+            uint64_t elo = 0, ehi = 0;  // exponent byte of weight i: byte i & 7 of (i < 8 ? elo : ehi)
             uint32_t ra = q0, rb = b1, rc = b2;
             const uint32_t pw0 = palg[0], pw1 = palg[1];
+#pragma unroll 1
             for (int i = 0; i < 16; ++i) {
                 const uint32_t code = (T0 >> (2 * i)) & 3u;
                 uint32_t e;
@@ -1083,12 +1183,19 @@ __global__ __launch_bounds__(kSipThreads, M == 8 ? 3 : 6) void k_gemv_gulp(const
                             e = has_term ? gulp_field(s3, rc++, 8) : 0u;
                     }
                 }
-                ex[i] = e;
+                const uint64_t v = (uint64_t)e << (8 * (i & 7));
+                if (i < 8)
+                    elo |= v;
+                else
+                    ehi |= v;
             }
-            E0 = make_uint2((ex[0] << 7) | (ex[1] << 23), (ex[2] << 7) | (ex[3] << 23));
-            E1 = make_uint2((ex[4] << 7) | (ex[5] << 23), (ex[6] << 7) | (ex[7] << 23));
-            E2 = make_uint2((ex[8] << 7) | (ex[9] << 23), (ex[10] << 7) | (ex[11] << 23));
-            E3 = make_uint2((ex[12] << 7) | (ex[13] << 23), (ex[14] << 7) | (ex[15] << 23));
+            // exponent bytes 4g, 4g + 1 -> the pair E_g.x, 4g + 2, 4g + 3 -> E_g.y
+            const uint32_t eb0 = (uint32_t)elo, eb1 = (uint32_t)(elo >> 32), eb2 = (uint32_t)ehi,
+                           eb3 = (uint32_t)(ehi >> 32);
+            E0 = make_uint2(__builtin_amdgcn_perm(0u, eb0, 0x0C010C00u) << 7, __builtin_amdgcn_perm(0u, eb0, 0x0C030C02u) << 7);
+            E1 = make_uint2(__builtin_amdgcn_perm(0u, eb1, 0x0C010C00u) << 7, __builtin_amdgcn_perm(0u, eb1, 0x0C030C02u) << 7);
+            E2 = make_uint2(__builtin_amdgcn_perm(0u, eb2, 0x0C010C00u) << 7, __builtin_amdgcn_perm(0u, eb2, 0x0C030C02u) << 7);
+            E3 = make_uint2(__builtin_amdgcn_perm(0u, eb3, 0x0C010C00u) << 7, __builtin_amdgcn_perm(0u, eb3, 0x0C030C02u) << 7);
         } else {
             // lane j resolves tier-1 escapes 2j, 2j + 1: their 4-bit codes sit in
             // tier-2 word j / 4 (the one this lane loaded), code 15 escaping to
@@ -1151,8 +1258,8 @@ __global__ __launch_bounds__(kSipThreads, M == 8 ? 3 : 6) void k_gemv_gulp(const
 #pragma unroll
             for (int m = 0; m < M; ++m) {
                 uint4 ya, yc;
-                __builtin_memcpy(&ya, xb + m * sh.cols, 16);
-                __builtin_memcpy(&yc, xb + m * sh.cols + 512, 16);
+                __builtin_memcpy(&ya, xb + m * sh.phase_blocks * 1024, 16);
+                __builtin_memcpy(&yc, xb + m * sh.phase_blocks * 1024 + 512, 16);
                 float a = acc[m];
                 a = dot2(wp[0], ya.x, a);
                 a = dot2(wp[1], ya.y, a);
@@ -1167,18 +1274,18 @@ __global__ __launch_bounds__(kSipThreads, M == 8 ? 3 : 6) void k_gemv_gulp(const
         if (c.j + 1 == sh.seg_blocks) {
             if (M == 1) {
                 const float s = wave_sum_dpp(acc0 + acc1);
-                if (lane == 0) red[c.u] = s;
+                if (lane == 0) red[c.slot] = s;
                 acc0 = acc1 = 0.0f;
             } else {
 #pragma unroll
                 for (int m = 0; m < M; ++m) {
                     const float s = wave_sum_dpp(acc[m]);
-                    if (lane == 0) red[c.u * M + m] = s;
+                    if (lane == 0) red[c.slot * M + m] = s;
                     acc[m] = 0.0f;
                 }
             }
         }
-        sip_next<false>(sh, c, sp);
+        sip_next<false>(sh, c, wk, sp);
     };
     const uint32_t my_units = wv < units ? (units - wv + kSipWaves - 1) / kSipWaves : 0;
     const uint32_t items = my_units * sh.seg_blocks;
@@ -1204,6 +1311,8 @@ __global__ __launch_bounds__(kSipThreads, M == 8 ? 3 : 6) void k_gemv_gulp(const
     if (k < items) process(sA);
     GULP_WAIT(0, sB);
     if (k + 1 < items) process(sB);
+    if (PH)
+        while (cur_phase + 1 < sh.phases) phase_advance();
     __syncthreads();
     const void* bias = pick(g.bias, ia);
     void* out = pick(g.out, ia);
@@ -1309,14 +1418,79 @@ bool sip_eligible(const dmx_radix_tensor* t, const void* x, int x_dtype, uint32_
 // One launch of the sip kernel over n tensors of equal cols (already
 // checked). Returns 2 when the group cannot run as one launch (a row tile
 // taller than a tensor, or tables past the LDS), having launched nothing.
+// The work plan of a sip or gulp launch over the group's sh.rows rows:
+// two workgroups per CU where their LDS fits, else one (M = 8's registers
+// allow only one); T rows per workgroup; the fewest column phases P (a
+// divisor of NB) whose activation slice fits in LDS; within a phase, the
+// segments that give the fewest block-times per workgroup (a unit's
+// closing wave sum, one per activation row, costing about a quarter of a
+// block). `fixed` is the kernel's static LDS; a second exponent table is
+// added when a tile spans two tensors (allowed only with `allow_two`).
+// Returns false, planning nothing, when no plan fits.
+bool plan_launch(SipShape& sh, const SipGroup& g, uint32_t n, uint32_t min_rows, uint32_t M, size_t fixed,
+                 bool allow_two, uint32_t& grid_out, size_t& lds_out, bool& two_out) {
+    for (uint32_t per_cu = M == 8 ? 1 : 2; per_cu >= 1; --per_cu) {
+        uint32_t grid = std::min<uint32_t>(sh.rows, (uint32_t)cu_count() * per_cu);
+        const uint32_t T = (sh.rows + grid - 1) / grid;
+        grid = (sh.rows + T - 1) / T;
+        bool two = false;
+        for (uint32_t i = 1; i < n; ++i) two |= g.row0[i] % T != 0;
+        if (T <= min_rows && (allow_two || !two)) {
+            for (uint32_t P = 1; P <= sh.nb; ++P) {
+                if (sh.nb % P) continue;
+                if (P > 1 && M >= 4 && per_cu > 1) break;  // (phased kernels at M >= 4: one workgroup per CU)
+                const uint32_t K = sh.nb / P;
+                double best = 1e30;
+                uint32_t ps = 1;
+                for (uint32_t s = 1; s <= std::min<uint32_t>(K, kSipWaves); ++s) {
+                    if (K % s) continue;
+                    const double rounds = std::ceil((double)T * s / kSipWaves);
+                    const double cost = P * rounds * ((double)(K / s) + 0.25 * M);
+                    if (cost < best - 1e-9) {
+                        best = cost;
+                        ps = s;
+                    }
+                }
+                if (two && P > 1) break;  // (a tile spanning two tensors keeps every activation column resident)
+                const size_t head = 2 * (size_t)M * K * 1024 + (((size_t)T * P * ps * M * 4 + 15) & ~(size_t)15);
+                const size_t lds = head + (two ? kTableBytes : 0);
+                if ((lds + fixed) * per_cu > 160 * 1024) continue;
+                sh.rows_per_wg = T;
+                sh.phases = P;
+                sh.phase_blocks = K;
+                sh.psegs = ps;
+                sh.segs = P * ps;
+                sh.seg_blocks = K / ps;
+                sh.phase_units = T * ps;
+                const uint32_t pu = T * ps, rem = kSipWaves % pu;
+                sh.dp = kSipWaves / pu;
+                sh.dr = rem / ps;
+                sh.ds = rem - sh.dr * ps;
+                sh.tbl2_lds = two ? (uint32_t)head : 0u;
+                grid_out = grid;
+                lds_out = lds;
+                two_out = two;
+                return true;
+            }
+        }
+        if (per_cu == 1) break;
+    }
+    return false;
+}
+
 typedef void (*SipKernel)(const SipGroup, const uint16_t*, const SipShape);
 
-// k_gemv_sip<two, M> for M = 1, 2, 4, 8 (index 0..3)
-SipKernel sip_kernel(bool two, int mi) {
-    static const SipKernel table[2][4] = {
-        {k_gemv_sip<false, 1>, k_gemv_sip<false, 2>, k_gemv_sip<false, 4>, k_gemv_sip<false, 8>},
-        {k_gemv_sip<true, 1>, k_gemv_sip<true, 2>, k_gemv_sip<true, 4>, k_gemv_sip<true, 8>}};
-    return table[two ? 1 : 0][mi];
+// k_gemv_sip for M = 1, 2, 4, 8 (mi 0..3): one column phase (spanning tiles
+// or not: kind 0, 1) or several (kind 2; tiles never span then)
+SipKernel sip_kernel(int kind, int mi) {
+    static const SipKernel table[3][4] = {
+        {k_gemv_sip<false, 1, false>, k_gemv_sip<false, 2, false>, k_gemv_sip<false, 4, false>,
+         k_gemv_sip<false, 8, false>},
+        {k_gemv_sip<true, 1, false>, k_gemv_sip<true, 2, false>, k_gemv_sip<true, 4, false>,
+         k_gemv_sip<true, 8, false>},
+        {k_gemv_sip<false, 1, true>, k_gemv_sip<false, 2, true>, k_gemv_sip<false, 4, true>,
+         k_gemv_sip<false, 8, true>}};
+    return table[kind][mi];
 }
 
 int launch_sip(const dmx_radix_tensor* const* ts, uint32_t n, const void* x, uint32_t m, const void* const* bias,
@@ -1352,45 +1526,14 @@ int launch_sip(const dmx_radix_tensor* const* ts, uint32_t n, const void* x, uin
     sh.m = m;
     sh.bias_dtype = bias_dtype;
     sh.out_dtype = out_dtype;
-    // one workgroup per slot (two per CU where their LDS fits, else one), T
-    // rows each; S segments per row so that the T * S units deal evenly to
-    // the waves
     const size_t fixed = kTableBytes + kSelBytes;
     uint32_t grid = 0;
     size_t lds = 0;
     bool two = false;
-    // (M = 8's registers allow one workgroup per CU)
-    for (uint32_t per_cu = M == 8 ? 1 : 2; per_cu >= 1; --per_cu) {
-        grid = std::min<uint32_t>(sh.rows, (uint32_t)cu_count() * per_cu);
-        sh.rows_per_wg = (sh.rows + grid - 1) / grid;
-        if (sh.rows_per_wg > min_rows) return 2;
-        grid = (sh.rows + sh.rows_per_wg - 1) / sh.rows_per_wg;
-        // S: the fewest block-times per workgroup, each of a unit's closing
-        // wave sums (one per activation row) costing about a quarter of a block
-        double best = 1e30;
-        sh.segs = 1;
-        for (uint32_t s = 1; s <= std::min<uint32_t>(sh.nb, kSipWaves); ++s) {
-            if (sh.nb % s) continue;
-            const double rounds = std::ceil((double)sh.rows_per_wg * s / kSipWaves);
-            const double cost = rounds * ((double)(sh.nb / s) + 0.25 * M);
-            if (cost < best - 1e-9) {
-                best = cost;
-                sh.segs = s;
-            }
-        }
-        sh.seg_blocks = sh.nb / sh.segs;
-        // a workgroup spans two tensors where a tensor starts inside its tile
-        two = false;
-        for (uint32_t i = 1; i < n; ++i) two |= g.row0[i] % sh.rows_per_wg != 0;
-        const size_t head = 2 * (size_t)M * sh.cols + (((size_t)sh.rows_per_wg * sh.segs * M * 4 + 15) & ~(size_t)15);
-        sh.tbl2_lds = two ? (uint32_t)head : 0u;
-        lds = head + (two ? kTableBytes : 0);
-        if ((lds + fixed) * per_cu <= 160 * 1024) break;
-        if (per_cu == 1) return 2;
-    }
+    if (!plan_launch(sh, g, n, min_rows, M, fixed, true, grid, lds, two)) return 2;
     static std::atomic<size_t> lds_opted{64 * 1024 - fixed};
     if (lds > lds_opted.load()) {
-        for (int t = 0; t < 2; ++t)
+        for (int t = 0; t < 3; ++t)
             for (int i = 0; i < 4; ++i) {
                 hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(sip_kernel(t, i)),
                                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
@@ -1398,7 +1541,7 @@ int launch_sip(const dmx_radix_tensor* const* ts, uint32_t n, const void* x, uin
             }
         lds_opted.store(lds);
     }
-    hipLaunchKernelGGL(sip_kernel(two, mi), dim3(grid), dim3(kSipThreads), lds, stream, g,
+    hipLaunchKernelGGL(sip_kernel(sh.phases > 1 ? 2 : two ? 1 : 0, mi), dim3(grid), dim3(kSipThreads), lds, stream, g,
                        static_cast<const uint16_t*>(x), sh);
     return launch_check(err, errn, "sip gemv launch");
 }
@@ -1415,9 +1558,11 @@ bool gulp_eligible(const dmx_radix_tensor* t, const void* x, int x_dtype, uint32
 
 typedef void (*GulpKernel)(const SipGroup, const uint16_t*, const SipShape);
 
-GulpKernel gulp_kernel(int mi) {
-    static const GulpKernel table[4] = {k_gemv_gulp<1>, k_gemv_gulp<2>, k_gemv_gulp<4>, k_gemv_gulp<8>};
-    return table[mi];
+GulpKernel gulp_kernel(bool phased, int mi) {
+    static const GulpKernel table[2][4] = {
+        {k_gemv_gulp<1, false>, k_gemv_gulp<2, false>, k_gemv_gulp<4, false>, k_gemv_gulp<8, false>},
+        {k_gemv_gulp<1, true>, k_gemv_gulp<2, true>, k_gemv_gulp<4, true>, k_gemv_gulp<8, true>}};
+    return table[phased ? 1 : 0][mi];
 }
 
 // One launch of the gulp kernel over n tensors of equal cols (already
@@ -1431,6 +1576,7 @@ int launch_gulp(const dmx_radix_tensor* const* ts, uint32_t n, const void* x, ui
     SipGroup g;
     SipShape sh;
     uint64_t total = 0;
+    uint32_t min_rows = ts[0]->rows;
     for (uint32_t i = 0; i < (uint32_t)kGroupMax; ++i) {
         const dmx_radix_tensor* t = ts[i < n ? i : n - 1];
         g.data[i] = t->data;
@@ -1440,7 +1586,10 @@ int launch_gulp(const dmx_radix_tensor* const* ts, uint32_t n, const void* x, ui
         g.bias[i] = bias ? bias[i < n ? i : n - 1] : nullptr;
         g.out[i] = out[i < n ? i : n - 1];
         g.row0[i] = (uint32_t)total;
-        if (i < n) total += t->rows;
+        if (i < n) {
+            total += t->rows;
+            min_rows = std::min(min_rows, t->rows);
+        }
     }
     if (total >= (1ull << 31)) return 2;
     for (uint32_t i = n; i <= (uint32_t)kGroupMax; ++i) g.row0[i] = (uint32_t)total;
@@ -1455,39 +1604,20 @@ int launch_gulp(const dmx_radix_tensor* const* ts, uint32_t n, const void* x, ui
     const size_t fixed = kGulpT0Bytes + kTableBytes + 13 * 16 * 8 + 16 + kSipWaves * kGulpX2Words * 4;
     uint32_t grid = 0;
     size_t lds = 0;
-    for (uint32_t per_cu = M == 8 ? 1 : 2; per_cu >= 1; --per_cu) {
-        grid = std::min<uint32_t>(sh.rows, (uint32_t)cu_count() * per_cu);
-        sh.rows_per_wg = (sh.rows + grid - 1) / grid;
-        grid = (sh.rows + sh.rows_per_wg - 1) / sh.rows_per_wg;
-        for (uint32_t i = 1; i < n; ++i)
-            if (g.row0[i] % sh.rows_per_wg) return 2;
-        double best = 1e30;
-        sh.segs = 1;
-        for (uint32_t s = 1; s <= std::min<uint32_t>(sh.nb, kSipWaves); ++s) {
-            if (sh.nb % s) continue;
-            const double rounds = std::ceil((double)sh.rows_per_wg * s / kSipWaves);
-            const double cost = rounds * ((double)(sh.nb / s) + 0.25 * M);
-            if (cost < best - 1e-9) {
-                best = cost;
-                sh.segs = s;
-            }
-        }
-        sh.seg_blocks = sh.nb / sh.segs;
-        lds = 2 * (size_t)M * sh.cols + (((size_t)sh.rows_per_wg * sh.segs * M * 4 + 15) & ~(size_t)15);
-        if ((lds + fixed) * per_cu <= 160 * 1024) break;
-        if (per_cu == 1) return 2;
-    }
+    bool two = false;
+    if (!plan_launch(sh, g, n, min_rows, M, fixed, false, grid, lds, two)) return 2;
     static std::atomic<size_t> lds_opted{64 * 1024 - fixed};
     if (lds > lds_opted.load()) {
-        for (int i = 0; i < 4; ++i) {
-            hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(gulp_kernel(i)),
-                                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-            if (e != hipSuccess) return fail_hip(err, errn, "gulp kernel LDS opt-in", e);
-        }
+        for (int t = 0; t < 2; ++t)
+            for (int i = 0; i < 4; ++i) {
+                hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(gulp_kernel(t, i)),
+                                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+                if (e != hipSuccess) return fail_hip(err, errn, "gulp kernel LDS opt-in", e);
+            }
         lds_opted.store(lds);
     }
-    hipLaunchKernelGGL(gulp_kernel(mi), dim3(grid), dim3(kSipThreads), lds, stream, g, static_cast<const uint16_t*>(x),
-                       sh);
+    hipLaunchKernelGGL(gulp_kernel(sh.phases > 1, mi), dim3(grid), dim3(kSipThreads), lds, stream, g,
+                       static_cast<const uint16_t*>(x), sh);
     return launch_check(err, errn, "gulp gemv launch");
 }
 
