@@ -536,19 +536,29 @@ __device__ __forceinline__ void sip_next(const SipShape& sh, SipCursor& c, const
 // x[16q + 8 .. 16q + 15], so a lane's two reads of its 16 activations each
 // cover 1 KB contiguously over the wave (no bank conflicts). A padding row
 // (m >= sh.m) repeats the last real row (its sums are never stored).
+//
+// The loads are written as instructions the compiler does not track (as the
+// payload loads are), so it adds no wait of its own for them: the caller
+// waits with an explicit vmcnt before the barrier that publishes xs. Each
+// wave loads whole 64-chunk runs (row_chunks is a multiple of 64), so M0,
+// the wave's LDS destination, is uniform.
+__device__ __forceinline__ void lds_load16(const void* g, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds) : "m0", "memory");
+}
+
 template <int M, int THREADS>
 __device__ __forceinline__ void load_x_slice(const SipShape& sh, const uint16_t* __restrict__ x, uint16_t* xs,
                                              uint32_t phase) {
-    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t lane = lane_id(), wbase = wave_id() * 64u;
     const uint32_t row_chunks = sh.phase_blocks * 128u, xchunks = sh.cols / 8, first = phase * row_chunks;
+    const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_ptr)xs;
 #pragma unroll
     for (uint32_t m = 0; m < (uint32_t)M; ++m) {
         const uint32_t src_row = min(m, sh.m - 1) * xchunks + first;
-        for (uint32_t j = threadIdx.x; j < row_chunks; j += THREADS) {
+        for (uint32_t jw = wbase; jw < row_chunks; jw += THREADS) {
+            const uint32_t j = jw + lane;
             const uint32_t q = j & 127u, src = src_row + ((j & ~127u) | (q < 64u ? 2u * q : 2u * (q - 64u) + 1u));
-            __builtin_amdgcn_global_load_lds((glb_ptr)(reinterpret_cast<const uint4*>(x) + src),
-                                             (lds_ptr)(reinterpret_cast<uint4*>(xs) + m * row_chunks + (j - lane)),
-                                             16, 0, 0);
+            lds_load16(reinterpret_cast<const uint4*>(x) + src, lds0 + 16u * (m * row_chunks + jw));
         }
     }
 }
@@ -685,8 +695,10 @@ __global__ __launch_bounds__(kSipThreads, (M == 8 || (PH && M == 4)) ? 3 : 6) vo
         sel2[i] = e;
         if (o == 0) sel[m] = e;
     }
-    // every wave's direct loads into LDS must land before any wave reads
-    __builtin_amdgcn_s_waitcnt(0);
+    // every wave's direct loads into LDS must land before any wave reads:
+    // they precede the two stages' 6 loads in the wave's queue, so vmcnt(6)
+    // completes them while the stages stay in flight
+    asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
     __syncthreads();
 
     const uint32_t keep = 0x807F807Fu;  // sign + mantissa bits of a bf16 pair, from the literal
@@ -1007,7 +1019,10 @@ __device__ __forceinline__ void gulp_tables(uint2* t0tab, uint2* t1tab, uint8_t*
         t1tab[i] = make_uint2((e[0] << 7) | (e[1] << 23) | (m1 << 3) | ((uint32_t)__builtin_popcount(m1) << 15),
                               (e[2] << 7) | (e[3] << 23));
     }
-    if (threadIdx.x < 4) reinterpret_cast<uint32_t*>(pal2)[threadIdx.x] = pw[2 + threadIdx.x];
+    // (uniform scalar reads: a vector load here would need a vmcnt(0) wait,
+    // which would also wait out the payload loads already in flight)
+    const uint32_t p2 = pw[2], p3 = pw[3], p4 = pw[4], p5 = pw[5], t = threadIdx.x;
+    if (t < 4) reinterpret_cast<uint32_t*>(pal2)[t] = t == 0 ? p2 : t == 1 ? p3 : t == 2 ? p4 : p5;
 }
 
 template <int M, bool PH>
@@ -1086,7 +1101,8 @@ __global__ __launch_bounds__(kSipThreads, (M == 8 || (PH && M == 4)) ? 3 : 6) vo
         for (uint32_t k = 0, r = o; k < 4; ++k) b[k] = (m >> k) & 1 ? (r++ & 7) : 0x0Cu;
         sel2[i] = make_uint2(b[0] | 0x0C00u | (b[1] << 16) | 0x0C000000u, b[2] | 0x0C00u | (b[3] << 16) | 0x0C000000u);
     }
-    __builtin_amdgcn_s_waitcnt(0);
+    // the activation's direct loads precede the two stages' 10 loads
+    asm volatile("s_waitcnt vmcnt(10)" ::: "memory");
     __syncthreads();
 
     const uint32_t keep = 0x807F807Fu;
