@@ -325,6 +325,110 @@ __device__ __forceinline__ float wave_sum_dpp(float v) {
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
 
+// Sum over each row of 16 lanes (inclusive DPP scan); lane 15 of the row
+// holds it.
+__device__ __forceinline__ float row_sum16(float v) {
+#define DMX_DPP_ADD(ctrl) \
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), ctrl, 0xF, 0xF, false))
+    DMX_DPP_ADD(0x111);
+    DMX_DPP_ADD(0x112);
+    DMX_DPP_ADD(0x114);
+    DMX_DPP_ADD(0x118);
+#undef DMX_DPP_ADD
+    return v;
+}
+
+// Verify rows (M = 4 or 8) on the matrix cores. v_mfma_f32_16x16x32_bf16
+// leaves in lane L, register v:
+//   D[L][v] += sum over g < 4, t < 8 of A[16 g + 4 (L / 16) + v][t] * B[16 g + L % 16][t]
+// where X[l][t] is element t of lane l's 8-element operand. B is the block's
+// decoded weights: half h of lane l is its weights 8h .. 8h + 7 (pair words
+// 4h .. 4h + 3). Variant s < M of A gives lane 16 g + i the M activation row
+// i / R at the columns of lane 16 g + R s + i % R's half-h weights
+// (R = 16 / M). So D_s, lane L, register v holds a dot product of matching
+// columns exactly where L % 16 == R s + (4 (L / 16) + v) % R: for M = 4 one
+// register per lane (s = (L % 16) / 4, v = L % 4, row L / 16); for M = 8 two
+// (s = (L % 16) / 2, v = L % 2 and 2 + L % 2, rows 2 (L / 16) and
+// 2 (L / 16) + 1). The other entries pair unrelated columns and are dropped.
+// Each lane's A operand is one 16-byte LDS read; the row stride of 2 K KB
+// plus 256 / M bytes puts the 16 lanes of a read on distinct banks.
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// The lane's A byte offset within an activation column block: row i / R,
+// the 16-byte chunk of column lane 16 g + i % R.
+template <int M>
+__device__ __forceinline__ uint32_t mf_lane_offset(uint32_t lane, uint32_t xrow) {
+    constexpr uint32_t R = 16 / M;
+    const uint32_t i = lane & 15u;
+    return (i / R) * (2u * xrow) + 16u * ((lane & ~15u) + i % R);
+}
+
+// One block into the M variants' accumulators: xa is the lane's A address
+// in the block's column block (chunk q of a 1024-column block holds columns
+// 16q .. 16q + 7 and chunk 64 + q columns 16q + 8 .. 16q + 15).
+template <int M>
+__device__ __forceinline__ void mf_block(f32x4 (&d)[M], const uint8_t* xa, const uint32_t (&wp)[8]) {
+    constexpr uint32_t R = 16 / M;
+    const bf16x8_t b0 = __builtin_bit_cast(bf16x8_t, make_uint4(wp[0], wp[1], wp[2], wp[3]));
+    const bf16x8_t b1 = __builtin_bit_cast(bf16x8_t, make_uint4(wp[4], wp[5], wp[6], wp[7]));
+#pragma unroll
+    for (int s = 0; s < M; ++s) {
+        bf16x8_t a;
+        __builtin_memcpy(&a, xa + 16 * R * s, 16);
+        d[s] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b0, d[s], 0, 0, 0);
+    }
+#pragma unroll
+    for (int s = 0; s < M; ++s) {
+        bf16x8_t a;
+        __builtin_memcpy(&a, xa + 1024 + 16 * R * s, 16);
+        d[s] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b1, d[s], 0, 0, 0);
+    }
+}
+
+// A unit's M row sums from the accumulators (then cleared): each lane's
+// matching entries, summed over the 16 lanes of its row group, into
+// out[0 .. M).
+template <int M>
+__device__ __forceinline__ void mf_unit_end(f32x4 (&d)[M], float* out, uint32_t lane) {
+    constexpr uint32_t R = 16 / M;
+    const uint32_t j = lane & 15u, s = j / R;
+    // d[s] by selects on the bits of s, over register copies: selects over
+    // the array itself would be folded into an indexed copy through scratch
+    f32x4 r[M];
+#pragma unroll
+    for (int k = 0; k < M; ++k) {
+        r[k] = d[k];
+        asm volatile("" : "+v"(r[k]));
+    }
+    const bool s0 = s & 1u, s1 = s & 2u;
+    f32x4 e = s1 ? (s0 ? r[3] : r[2]) : (s0 ? r[1] : r[0]);
+    if (M == 8) {
+        const f32x4 e2 = s1 ? (s0 ? r[M - 1] : r[M - 2]) : (s0 ? r[M - 3] : r[M - 4]);
+        e = (s & 4u) ? e2 : e;
+    }
+    const float lo = (j & 1u) ? e[1] : e[0], hi = (j & 1u) ? e[3] : e[2];
+    if (M == 4) {
+        const float v = row_sum16((j & 2u) ? hi : lo);
+        if (j == 15) out[lane >> 4] = v;
+    } else {
+        const float v0 = row_sum16(lo), v1 = row_sum16(hi);
+        if (j == 15) {
+            out[2 * (lane >> 4)] = v0;
+            out[2 * (lane >> 4) + 1] = v1;
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < M; ++k) d[k] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+}
+
+// Verify rows go to the matrix cores where that is faster: sip at M = 4 and
+// 8, gulp at M = 8. Gulp at M = 4 keeps v_dot2: its accumulators would take
+// it past the 80 registers of 6 waves per SIMD, and the decode, bound by
+// latency, loses more from 5 waves than the products gain.
+__host__ __device__ constexpr bool sip_mfma(int M) { return M >= 4; }
+__host__ __device__ constexpr bool gulp_mfma(int M) { return M >= 8; }
+
 // A group of sip tensors that share the activation (the q/k/v or gate/up
 // projections of a layer) runs as one launch: their rows form one row
 // space, tensor i's from row0[i]. The host keeps the row tile no taller than
@@ -351,6 +455,8 @@ struct SipShape {
     uint32_t seg_blocks;      // L = NB / S
     uint32_t phases;          // P: column phases (1 = every activation column resident in LDS)
     uint32_t phase_blocks;    // K = NB / P column blocks of activations in LDS at a time
+    uint32_t xrow;            // LDS stride of the activation rows, in bf16: K * 1024, plus 128 / M for the matrix cores
+    uint32_t waves;           // W: waves per workgroup
     uint32_t psegs;           // segments per phase
     uint32_t phase_units;     // T * psegs units per phase
     uint32_t dp, dr, ds;      // a wave's step of W units in a full tile: phases, rows, segments
@@ -472,8 +578,8 @@ __device__ __forceinline__ SipWalk sip_walk(const SipShape& sh, uint32_t nrows) 
         w.dr = sh.dr;
         w.ds = sh.ds;
     } else {
-        const uint32_t pu = nrows * sh.psegs, rem = kSipWaves % pu;
-        w.dp = kSipWaves / pu;
+        const uint32_t pu = nrows * sh.psegs, rem = sh.waves % pu;
+        w.dp = sh.waves / pu;
         w.dr = rem / sh.psegs;
         w.ds = rem - w.dr * sh.psegs;
     }
@@ -531,7 +637,7 @@ __device__ __forceinline__ void sip_next(const SipShape& sh, SipCursor& c, const
 }
 
 // Rows 0..M-1 of x, columns [phase K 1024, (phase + 1) K 1024), into LDS
-// by direct loads: row m at xs + m K 1024; within each 1024-column block,
+// by direct loads: row m at xs + m xrow; within each 1024-column block,
 // 16-byte chunk q < 64 holds x[16q .. 16q + 7] and chunk 64 + q holds
 // x[16q + 8 .. 16q + 15], so a lane's two reads of its 16 activations each
 // cover 1 KB contiguously over the wave (no bank conflicts). A padding row
@@ -558,7 +664,7 @@ __device__ __forceinline__ void load_x_slice(const SipShape& sh, const uint16_t*
         for (uint32_t jw = wbase; jw < row_chunks; jw += THREADS) {
             const uint32_t j = jw + lane;
             const uint32_t q = j & 127u, src = src_row + ((j & ~127u) | (q < 64u ? 2u * q : 2u * (q - 64u) + 1u));
-            lds_load16(reinterpret_cast<const uint4*>(x) + src, lds0 + 16u * (m * row_chunks + jw));
+            lds_load16(reinterpret_cast<const uint4*>(x) + src, lds0 + 2u * m * sh.xrow + 16u * jw);
         }
     }
 }
@@ -605,7 +711,9 @@ __global__ __launch_bounds__(kSipThreads, (M == 8 || (PH && M == 4)) ? 3 : 6) vo
     __shared__ uint2 sel2[13 * 16];
     extern __shared__ __align__(16) uint8_t lds_dyn[];
     uint16_t* xs = reinterpret_cast<uint16_t*>(lds_dyn);
-    float* red = reinterpret_cast<float*>(lds_dyn + 2 * M * sh.phase_blocks * 1024);
+    // (a multiple of 8 bf16, stated so that 16-byte LDS reads of the rows stay whole)
+    const uint32_t xrow = sh.xrow & ~7u;
+    float* red = reinterpret_cast<float*>(lds_dyn + 2 * M * xrow);
     uint2* tbl2 = reinterpret_cast<uint2*>(lds_dyn + sh.tbl2_lds);
 
     const uint32_t wv = wave_id(), lane = lane_id();
@@ -704,9 +812,15 @@ __global__ __launch_bounds__(kSipThreads, (M == 8 || (PH && M == 4)) ? 3 : 6) vo
     const uint32_t keep = 0x807F807Fu;  // sign + mantissa bits of a bf16 pair, from the literal
     // M = 1 keeps two accumulator chains; M > 1 one per row
     float acc0 = 0.0f, acc1 = 0.0f;
-    float acc[M];
+    constexpr bool MF = sip_mfma(M);  // verify rows on the matrix cores
+    constexpr int MA = MF ? 1 : M, MD = MF ? M : 1;
+    float acc[MA];
 #pragma unroll
-    for (int m = 0; m < M; ++m) acc[m] = 0.0f;
+    for (int m = 0; m < MA; ++m) acc[m] = 0.0f;
+    f32x4 dacc[MD];
+#pragma unroll
+    for (int m = 0; m < MD; ++m) dacc[m] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    const uint32_t mf_off = MF ? mf_lane_offset<MD>(lane, xrow) : 0u;
     // one block of the wave's work, from its loaded stage
     // column phases: every wave walks all of them in order (so the barriers
     // match); a phase's activations replace the last one's once every wave
@@ -813,12 +927,14 @@ __global__ __launch_bounds__(kSipThreads, (M == 8 || (PH && M == 4)) ? 3 : 6) vo
             acc1 = dot2(wp[5], xc.y, acc1);
             acc0 = dot2(wp[6], xc.z, acc0);
             acc1 = dot2(wp[7], xc.w, acc1);
+        } else if (MF) {
+            mf_block<MD>(dacc, reinterpret_cast<const uint8_t*>(xs) + mf_off + c.cb * 2048, wp);
         } else {
 #pragma unroll
-            for (int m = 0; m < M; ++m) {
+            for (int m = 0; m < MA; ++m) {
                 uint4 ya, yc;
-                __builtin_memcpy(&ya, xb + m * sh.phase_blocks * 1024, 16);
-                __builtin_memcpy(&yc, xb + m * sh.phase_blocks * 1024 + 512, 16);
+                __builtin_memcpy(&ya, xb + m * xrow, 16);
+                __builtin_memcpy(&yc, xb + m * xrow + 512, 16);
                 float a = acc[m];
                 a = dot2(wp[0], ya.x, a);
                 a = dot2(wp[1], ya.y, a);
@@ -836,9 +952,11 @@ __global__ __launch_bounds__(kSipThreads, (M == 8 || (PH && M == 4)) ? 3 : 6) vo
                 const float s = wave_sum_dpp(acc0 + acc1);
                 if (lane == 0) red[c.slot] = s;
                 acc0 = acc1 = 0.0f;
+            } else if (MF) {
+                mf_unit_end<MD>(dacc, red + c.slot * M, lane);
             } else {
 #pragma unroll
-                for (int m = 0; m < M; ++m) {
+                for (int m = 0; m < MA; ++m) {
                     const float s = wave_sum_dpp(acc[m]);
                     if (lane == 0) red[c.slot * M + m] = s;
                     acc[m] = 0.0f;
@@ -992,10 +1110,11 @@ __device__ __forceinline__ uint32_t gulp_field(const uint32_t* p, uint32_t i, ui
 //       order by the escaped positions of m0 (others 0), with m1 (the
 //       positions whose tier-1 code escapes) << 3 | popcount(m1) << 15;
 //   pal2[c]: tier 2's bytes.
+template <int THREADS>
 __device__ __forceinline__ void gulp_tables(uint2* t0tab, uint2* t1tab, uint8_t* pal2, const uint32_t* palette) {
     const const_u32_ptr pw = (const_u32_ptr)palette;
     const uint32_t p0 = pw[0], p1 = pw[1];
-    for (uint32_t i = threadIdx.x; i < 256; i += kSipThreads) {
+    for (uint32_t i = threadIdx.x; i < 256; i += THREADS) {
         uint32_t e[4], m = 0;
         for (uint32_t k = 0; k < 4; ++k) {
             const uint32_t c = (i >> (2 * k)) & 3u;
@@ -1005,7 +1124,7 @@ __device__ __forceinline__ void gulp_tables(uint2* t0tab, uint2* t1tab, uint8_t*
         t0tab[i] = make_uint2((e[0] << 7) | (e[1] << 23) | (m << 3) | ((2u * __builtin_popcount(m)) << 15),
                               (e[2] << 7) | (e[3] << 23));
     }
-    for (uint32_t i = threadIdx.x; i < 4096; i += kSipThreads) {
+    for (uint32_t i = threadIdx.x; i < 4096; i += THREADS) {
         const uint32_t m0 = i & 15u, codes = i >> 4;
         uint32_t e[4], m1 = 0, r = 0;
         for (uint32_t k = 0; k < 4; ++k) {
@@ -1028,14 +1147,17 @@ __device__ __forceinline__ void gulp_tables(uint2* t0tab, uint2* t1tab, uint8_t*
 template <int M, bool PH>
 __global__ __launch_bounds__(kSipThreads, (M == 8 || (PH && M == 4)) ? 3 : 6) void k_gemv_gulp(const SipGroup g, const uint16_t* __restrict__ x,
                                                                         const SipShape sh) {
+    constexpr int W = kSipWaves, TH = kSipThreads;
     __shared__ uint2 t0tab[256];
     __shared__ uint2 t1tab[4096];
     __shared__ uint2 sel2[13 * 16];
     __shared__ uint32_t pal2w[4];
-    __shared__ uint32_t x2_all[kSipWaves * kGulpX2Words];
+    __shared__ uint32_t x2_all[W * kGulpX2Words];
     extern __shared__ __align__(16) uint8_t lds_dyn[];
     uint16_t* xs = reinterpret_cast<uint16_t*>(lds_dyn);
-    float* red = reinterpret_cast<float*>(lds_dyn + 2 * M * sh.phase_blocks * 1024);
+    // (a multiple of 8 bf16, stated so that 16-byte LDS reads of the rows stay whole)
+    const uint32_t xrow = sh.xrow & ~7u;
+    float* red = reinterpret_cast<float*>(lds_dyn + 2 * M * xrow);
     const uint8_t* pal2 = reinterpret_cast<const uint8_t*>(pal2w);
 
     const uint32_t wv = wave_id(), lane = lane_id();
@@ -1062,7 +1184,7 @@ __global__ __launch_bounds__(kSipThreads, (M == 8 || (PH && M == 4)) ? 3 : 6) vo
     uint32_t* x2 = x2_all + wv * kGulpX2Words;
 
     // the activation rows (first column phase), as in the sip kernel
-    load_x_slice<M, kSipThreads>(sh, x, xs, 0);
+    load_x_slice<M, TH>(sh, x, xs, 0);
 
     SipCursor p, c;
     const SipWalk wk = sip_walk(sh, nrows);
@@ -1094,8 +1216,8 @@ __global__ __launch_bounds__(kSipThreads, (M == 8 || (PH && M == 4)) ? 3 : 6) vo
     __builtin_amdgcn_sched_barrier(0);
     GulpStage sC;
 
-    gulp_tables(t0tab, t1tab, reinterpret_cast<uint8_t*>(pal2w), pick(g.palette, ia));
-    for (uint32_t i = threadIdx.x; i < 13 * 16; i += kSipThreads) {
+    gulp_tables<TH>(t0tab, t1tab, reinterpret_cast<uint8_t*>(pal2w), pick(g.palette, ia));
+    for (uint32_t i = threadIdx.x; i < 13 * 16; i += TH) {
         const uint32_t m = i & 15, o = i >> 4;
         uint32_t b[4];
         for (uint32_t k = 0, r = o; k < 4; ++k) b[k] = (m >> k) & 1 ? (r++ & 7) : 0x0Cu;
@@ -1108,9 +1230,15 @@ __global__ __launch_bounds__(kSipThreads, (M == 8 || (PH && M == 4)) ? 3 : 6) vo
     const uint32_t keep = 0x807F807Fu;
     const uint32_t* palg = pick(g.palette, ia);
     float acc0 = 0.0f, acc1 = 0.0f;
-    float acc[M];
+    constexpr bool MF = gulp_mfma(M);  // verify rows on the matrix cores
+    constexpr int MA = MF ? 1 : M, MD = MF ? M : 1;
+    float acc[MA];
 #pragma unroll
-    for (int m = 0; m < M; ++m) acc[m] = 0.0f;
+    for (int m = 0; m < MA; ++m) acc[m] = 0.0f;
+    f32x4 dacc[MD];
+#pragma unroll
+    for (int m = 0; m < MD; ++m) dacc[m] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    const uint32_t mf_off = MF ? mf_lane_offset<MD>(lane, xrow) : 0u;
 
     // column phases: every wave walks all of them in order (so the barriers
     // match); a phase's activations replace the last one's once every wave
@@ -1119,7 +1247,7 @@ __global__ __launch_bounds__(kSipThreads, (M == 8 || (PH && M == 4)) ? 3 : 6) vo
     auto phase_advance = [&]() {
         __syncthreads();
         ++cur_phase;
-        load_x_slice<M, kSipThreads>(sh, x, xs, cur_phase);
+        load_x_slice<M, TH>(sh, x, xs, cur_phase);
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
     };
@@ -1270,12 +1398,14 @@ __global__ __launch_bounds__(kSipThreads, (M == 8 || (PH && M == 4)) ? 3 : 6) vo
             acc1 = dot2(wp[5], xc.y, acc1);
             acc0 = dot2(wp[6], xc.z, acc0);
             acc1 = dot2(wp[7], xc.w, acc1);
+        } else if (MF) {
+            mf_block<MD>(dacc, reinterpret_cast<const uint8_t*>(xs) + mf_off + c.cb * 2048, wp);
         } else {
 #pragma unroll
-            for (int m = 0; m < M; ++m) {
+            for (int m = 0; m < MA; ++m) {
                 uint4 ya, yc;
-                __builtin_memcpy(&ya, xb + m * sh.phase_blocks * 1024, 16);
-                __builtin_memcpy(&yc, xb + m * sh.phase_blocks * 1024 + 512, 16);
+                __builtin_memcpy(&ya, xb + m * xrow, 16);
+                __builtin_memcpy(&yc, xb + m * xrow + 512, 16);
                 float a = acc[m];
                 a = dot2(wp[0], ya.x, a);
                 a = dot2(wp[1], ya.y, a);
@@ -1292,9 +1422,11 @@ __global__ __launch_bounds__(kSipThreads, (M == 8 || (PH && M == 4)) ? 3 : 6) vo
                 const float s = wave_sum_dpp(acc0 + acc1);
                 if (lane == 0) red[c.slot] = s;
                 acc0 = acc1 = 0.0f;
+            } else if (MF) {
+                mf_unit_end<MD>(dacc, red + c.slot * M, lane);
             } else {
 #pragma unroll
-                for (int m = 0; m < M; ++m) {
+                for (int m = 0; m < MA; ++m) {
                     const float s = wave_sum_dpp(acc[m]);
                     if (lane == 0) red[c.slot * M + m] = s;
                     acc[m] = 0.0f;
@@ -1303,7 +1435,7 @@ __global__ __launch_bounds__(kSipThreads, (M == 8 || (PH && M == 4)) ? 3 : 6) vo
         }
         sip_next<false>(sh, c, wk, sp);
     };
-    const uint32_t my_units = wv < units ? (units - wv + kSipWaves - 1) / kSipWaves : 0;
+    const uint32_t my_units = wv < units ? (units - wv + W - 1) / W : 0;
     const uint32_t items = my_units * sh.seg_blocks;
     uint32_t k = 0;
     for (; k + 3 <= items; k += 3) {
@@ -1333,7 +1465,7 @@ __global__ __launch_bounds__(kSipThreads, (M == 8 || (PH && M == 4)) ? 3 : 6) vo
     const void* bias = pick(g.bias, ia);
     void* out = pick(g.out, ia);
     const uint32_t rows_t = row_n - row_a;
-    for (uint32_t i = threadIdx.x; i < nrows * sh.m; i += kSipThreads) {
+    for (uint32_t i = threadIdx.x; i < nrows * sh.m; i += TH) {
         const uint32_t m = i / nrows, t = i - m * nrows;
         float sum = 0.0f;
         for (uint32_t k = 0; k < sh.segs; ++k) sum += red[(t * sh.segs + k) * M + m];
@@ -1440,11 +1572,13 @@ bool sip_eligible(const dmx_radix_tensor* t, const void* x, int x_dtype, uint32_
 // divisor of NB) whose activation slice fits in LDS; within a phase, the
 // segments that give the fewest block-times per workgroup (a unit's
 // closing wave sum, one per activation row, costing about a quarter of a
-// block). `fixed` is the kernel's static LDS; a second exponent table is
-// added when a tile spans two tensors (allowed only with `allow_two`).
-// Returns false, planning nothing, when no plan fits.
-bool plan_launch(SipShape& sh, const SipGroup& g, uint32_t n, uint32_t min_rows, uint32_t M, size_t fixed,
-                 bool allow_two, uint32_t& grid_out, size_t& lds_out, bool& two_out) {
+// block). W is the kernel's waves per workgroup, mf whether its verify rows
+// use the matrix cores (their activation rows get a padded stride), `fixed`
+// its static LDS; a second exponent table is added when a tile spans two tensors (allowed
+// only with `allow_two`). Returns false, planning nothing, when no plan
+// fits.
+bool plan_launch(SipShape& sh, const SipGroup& g, uint32_t n, uint32_t min_rows, uint32_t M, uint32_t W,
+                 bool mf, size_t fixed, bool allow_two, uint32_t& grid_out, size_t& lds_out, bool& two_out) {
     for (uint32_t per_cu = M == 8 ? 1 : 2; per_cu >= 1; --per_cu) {
         uint32_t grid = std::min<uint32_t>(sh.rows, (uint32_t)cu_count() * per_cu);
         const uint32_t T = (sh.rows + grid - 1) / grid;
@@ -1458,9 +1592,9 @@ bool plan_launch(SipShape& sh, const SipGroup& g, uint32_t n, uint32_t min_rows,
                 const uint32_t K = sh.nb / P;
                 double best = 1e30;
                 uint32_t ps = 1;
-                for (uint32_t s = 1; s <= std::min<uint32_t>(K, kSipWaves); ++s) {
+                for (uint32_t s = 1; s <= std::min<uint32_t>(K, W); ++s) {
                     if (K % s) continue;
-                    const double rounds = std::ceil((double)T * s / kSipWaves);
+                    const double rounds = std::ceil((double)T * s / W);
                     const double cost = P * rounds * ((double)(K / s) + 0.25 * M);
                     if (cost < best - 1e-9) {
                         best = cost;
@@ -1468,18 +1602,21 @@ bool plan_launch(SipShape& sh, const SipGroup& g, uint32_t n, uint32_t min_rows,
                     }
                 }
                 if (two && P > 1) break;  // (a tile spanning two tensors keeps every activation column resident)
-                const size_t head = 2 * (size_t)M * K * 1024 + (((size_t)T * P * ps * M * 4 + 15) & ~(size_t)15);
+                const uint32_t xrow = K * 1024 + (mf ? 128 / M : 0);
+                const size_t head = 2 * (size_t)M * xrow + (((size_t)T * P * ps * M * 4 + 15) & ~(size_t)15);
                 const size_t lds = head + (two ? kTableBytes : 0);
                 if ((lds + fixed) * per_cu > 160 * 1024) continue;
                 sh.rows_per_wg = T;
                 sh.phases = P;
                 sh.phase_blocks = K;
+                sh.xrow = xrow;
+                sh.waves = W;
                 sh.psegs = ps;
                 sh.segs = P * ps;
                 sh.seg_blocks = K / ps;
                 sh.phase_units = T * ps;
-                const uint32_t pu = T * ps, rem = kSipWaves % pu;
-                sh.dp = kSipWaves / pu;
+                const uint32_t pu = T * ps, rem = W % pu;
+                sh.dp = W / pu;
                 sh.dr = rem / ps;
                 sh.ds = rem - sh.dr * ps;
                 sh.tbl2_lds = two ? (uint32_t)head : 0u;
@@ -1546,7 +1683,7 @@ int launch_sip(const dmx_radix_tensor* const* ts, uint32_t n, const void* x, uin
     uint32_t grid = 0;
     size_t lds = 0;
     bool two = false;
-    if (!plan_launch(sh, g, n, min_rows, M, fixed, true, grid, lds, two)) return 2;
+    if (!plan_launch(sh, g, n, min_rows, M, kSipWaves, sip_mfma((int)M), fixed, true, grid, lds, two)) return 2;
     static std::atomic<size_t> lds_opted{64 * 1024 - fixed};
     if (lds > lds_opted.load()) {
         for (int t = 0; t < 3; ++t)
@@ -1621,7 +1758,7 @@ int launch_gulp(const dmx_radix_tensor* const* ts, uint32_t n, const void* x, ui
     uint32_t grid = 0;
     size_t lds = 0;
     bool two = false;
-    if (!plan_launch(sh, g, n, min_rows, M, fixed, false, grid, lds, two)) return 2;
+    if (!plan_launch(sh, g, n, min_rows, M, kSipWaves, gulp_mfma((int)M), fixed, false, grid, lds, two)) return 2;
     static std::atomic<size_t> lds_opted{64 * 1024 - fixed};
     if (lds > lds_opted.load()) {
         for (int t = 0; t < 2; ++t)
