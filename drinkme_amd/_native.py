@@ -48,6 +48,7 @@ SIGNATURES = {
     "dmx_radix_prepare": (_I, [_TP, _P, _P, _P, _SZ]),
     "dmx_radix_gemv": (_I, [_TP, _P, _I, _U32, _P, _I, _P, _I, _P, _P, _SZ]),
     "dmx_radix_gemv_group": (_I, [_P, _U32, _P, _I, _U32, _P, _I, _P, _I, _P, _P, _SZ]),
+    "dmx_gemv_narrow": (_I, [_P, _U32, _U32, _P, _I, _U32, _P, _I, _P, _I, _P, _P, _SZ]),
     "dmx_radix_set_policy": (_I, [_I]),
     "dmx_synth_bf16": (_I, [_U64, _U64, _U64, ct.c_double, _U32, _P, _P, _SZ]),
 }

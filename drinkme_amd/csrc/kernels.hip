@@ -369,6 +369,7 @@ __device__ __forceinline__ uint32_t mf_lane_offset(uint32_t lane, uint32_t xrow)
 // 16q .. 16q + 7 and chunk 64 + q columns 16q + 8 .. 16q + 15).
 template <int M>
 __device__ __forceinline__ void mf_block(f32x4 (&d)[M], const uint8_t* xa, const uint32_t (&wp)[8]) {
+    static_assert(M == 4 || M == 8, "matrix-core verify rows: M = 4 or 8");
     constexpr uint32_t R = 16 / M;
     const bf16x8_t b0 = __builtin_bit_cast(bf16x8_t, make_uint4(wp[0], wp[1], wp[2], wp[3]));
     const bf16x8_t b1 = __builtin_bit_cast(bf16x8_t, make_uint4(wp[4], wp[5], wp[6], wp[7]));
@@ -391,6 +392,7 @@ __device__ __forceinline__ void mf_block(f32x4 (&d)[M], const uint8_t* xa, const
 // out[0 .. M).
 template <int M>
 __device__ __forceinline__ void mf_unit_end(f32x4 (&d)[M], float* out, uint32_t lane) {
+    static_assert(M == 4 || M == 8, "matrix-core verify rows: M = 4 or 8");
     constexpr uint32_t R = 16 / M;
     const uint32_t j = lane & 15u, s = j / R;
     // d[s] by selects on the bits of s, over register copies: selects over
@@ -647,9 +649,20 @@ __device__ __forceinline__ void sip_next(const SipShape& sh, SipCursor& c, const
 // payload loads are), so it adds no wait of its own for them: the caller
 // waits with an explicit vmcnt before the barrier that publishes xs. Each
 // wave loads whole 64-chunk runs (row_chunks is a multiple of 64), so M0,
-// the wave's LDS destination, is uniform.
+// the wave's LDS destination, is uniform. M0 is the compiler's register:
+// the statement restores it, and waits the one state an M0 write needs
+// before an LDS-bound load reads it.
 __device__ __forceinline__ void lds_load16(const void* g, uint32_t lds) {
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds) : "m0", "memory");
+    uint32_t saved;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %2\n\t"
+        "s_nop 0\n\t"
+        "global_load_lds_dwordx4 %1, off\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "v"(g), "s"(lds)
+        : "memory");
 }
 
 template <int M, int THREADS>
@@ -927,7 +940,7 @@ __global__ __launch_bounds__(kSipThreads, (M == 8 || (PH && M == 4)) ? 3 : 6) vo
             acc1 = dot2(wp[5], xc.y, acc1);
             acc0 = dot2(wp[6], xc.z, acc0);
             acc1 = dot2(wp[7], xc.w, acc1);
-        } else if (MF) {
+        } else if constexpr (MF) {
             mf_block<MD>(dacc, reinterpret_cast<const uint8_t*>(xs) + mf_off + c.cb * 2048, wp);
         } else {
 #pragma unroll
@@ -952,7 +965,7 @@ __global__ __launch_bounds__(kSipThreads, (M == 8 || (PH && M == 4)) ? 3 : 6) vo
                 const float s = wave_sum_dpp(acc0 + acc1);
                 if (lane == 0) red[c.slot] = s;
                 acc0 = acc1 = 0.0f;
-            } else if (MF) {
+            } else if constexpr (MF) {
                 mf_unit_end<MD>(dacc, red + c.slot * M, lane);
             } else {
 #pragma unroll
@@ -1398,7 +1411,7 @@ __global__ __launch_bounds__(kSipThreads, (M == 8 || (PH && M == 4)) ? 3 : 6) vo
             acc1 = dot2(wp[5], xc.y, acc1);
             acc0 = dot2(wp[6], xc.z, acc0);
             acc1 = dot2(wp[7], xc.w, acc1);
-        } else if (MF) {
+        } else if constexpr (MF) {
             mf_block<MD>(dacc, reinterpret_cast<const uint8_t*>(xs) + mf_off + c.cb * 2048, wp);
         } else {
 #pragma unroll
@@ -1422,7 +1435,7 @@ __global__ __launch_bounds__(kSipThreads, (M == 8 || (PH && M == 4)) ? 3 : 6) vo
                 const float s = wave_sum_dpp(acc0 + acc1);
                 if (lane == 0) red[c.slot] = s;
                 acc0 = acc1 = 0.0f;
-            } else if (MF) {
+            } else if constexpr (MF) {
                 mf_unit_end<MD>(dacc, red + c.slot * M, lane);
             } else {
 #pragma unroll
@@ -1471,6 +1484,94 @@ __global__ __launch_bounds__(kSipThreads, (M == 8 || (PH && M == 4)) ? 3 : 6) vo
         for (uint32_t k = 0; k < sh.segs; ++k) sum += red[(t * sh.segs + k) * M + m];
         if (bias) sum += load_elem(bias, sh.bias_dtype, lrow + t);
         store_elem(out, sh.out_dtype, (uint64_t)m * rows_t + lrow + t, sum);
+    }
+}
+
+// ------------------------------------------------------ raw bf16 GEMV --
+//
+// drinkme's _gemv_narrow (src/drinkme/codec/radix_ops.py:177-249), the
+// kernel of swap.NarrowLinear (src/drinkme/codec/swap.py:530-610): a raw
+// row-major bf16 weight [R, C], no decoder, against M <= 8 activation rows.
+// One workgroup of 256 threads per output row. Thread t takes the 8-column
+// chunks t, t + 256, ... of the row and, per activation row, adds x * w
+// over the chunk's columns in order with one fp32 fma each (16-byte loads
+// where the row and x allow, else element loads: the same sums). The 256
+// partials of a row are added in a fixed order (a DPP scan per wave, then
+// the four waves in turn), the bias in fp32, one rounding at the store.
+// Activation row m's arithmetic does not depend on M, so row m of an M-row
+// call is the one-row call bit for bit; and since widening bf16 to fp32 is
+// exact, a bf16 x gives the sums of its fp32 copy.
+constexpr int kNarrowThreads = 256;
+
+template <int M, bool VEC>
+__global__ __launch_bounds__(kNarrowThreads) void k_gemv_narrow(const uint16_t* __restrict__ w, uint32_t cols,
+                                                                const void* __restrict__ x, int x_dtype,
+                                                                const void* bias, int bias_dtype, void* out,
+                                                                int out_dtype, uint32_t rows) {
+    __shared__ float red[M][kNarrowThreads / kWave];
+    const uint32_t row = blockIdx.x;
+    const uint16_t* wr = w + (uint64_t)row * cols;
+    float acc[M];
+#pragma unroll
+    for (int m = 0; m < M; ++m) acc[m] = 0.0f;
+    const uint32_t chunks = (cols + 7) / 8;
+    for (uint32_t k = threadIdx.x; k < chunks; k += kNarrowThreads) {
+        const uint32_t c0 = 8 * k, n = min(8u, cols - c0);
+        float wf[8];
+        if (VEC) {
+            const uint4 v = *reinterpret_cast<const uint4*>(wr + c0);
+            const uint32_t u[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                wf[2 * e] = __uint_as_float(u[e] << 16);
+                wf[2 * e + 1] = __uint_as_float(u[e] & 0xFFFF0000u);
+            }
+        } else {
+#pragma unroll
+            for (uint32_t e = 0; e < 8; ++e) wf[e] = e < n ? bf16_bits_to_f32(wr[c0 + e]) : 0.0f;
+        }
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+            const uint64_t xo = (uint64_t)m * cols + c0;
+            float xf[8];
+            if (VEC && x_dtype == DMX_BF16) {
+                const uint4 v = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(x) + xo);
+                const uint32_t u[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    xf[2 * e] = __uint_as_float(u[e] << 16);
+                    xf[2 * e + 1] = __uint_as_float(u[e] & 0xFFFF0000u);
+                }
+            } else if (VEC) {
+                const float4 a = *reinterpret_cast<const float4*>(static_cast<const float*>(x) + xo);
+                const float4 b = *reinterpret_cast<const float4*>(static_cast<const float*>(x) + xo + 4);
+                xf[0] = a.x, xf[1] = a.y, xf[2] = a.z, xf[3] = a.w;
+                xf[4] = b.x, xf[5] = b.y, xf[6] = b.z, xf[7] = b.w;
+            } else {
+#pragma unroll
+                for (uint32_t e = 0; e < 8; ++e) xf[e] = e < n ? load_elem(x, x_dtype, xo + e) : 0.0f;
+            }
+            float a = acc[m];
+#pragma unroll
+            for (uint32_t e = 0; e < 8; ++e)
+                if (VEC || e < n) a = fmaf(xf[e], wf[e], a);
+            acc[m] = a;
+        }
+    }
+    const uint32_t wv = threadIdx.x / kWave;
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+        const float sum = wave_sum_dpp(acc[m]);
+        if (lane_id() == 0) red[m][wv] = sum;
+    }
+    __syncthreads();
+    if (threadIdx.x < (uint32_t)M) {
+        const uint32_t m = threadIdx.x;
+        float sum = 0.0f;
+#pragma unroll
+        for (int k = 0; k < kNarrowThreads / kWave; ++k) sum += red[m][k];
+        if (bias) sum += load_elem(bias, bias_dtype, row);
+        store_elem(out, out_dtype, (uint64_t)m * rows + row, sum);
     }
 }
 
@@ -1814,6 +1915,17 @@ int gemv_one(const dmx_radix_tensor* t, const Desc& d, const void* x, int x_dtyp
     return launch_check(err, errn, "generic gemv launch");
 }
 
+template <int M>
+void launch_narrow_m(bool vec, const uint16_t* w, uint32_t rows, uint32_t cols, const void* x, int x_dtype,
+                     const void* bias, int bias_dtype, void* out, int out_dtype, hipStream_t s) {
+    if (vec)
+        hipLaunchKernelGGL((k_gemv_narrow<M, true>), dim3(rows), dim3(kNarrowThreads), 0, s, w, cols, x, x_dtype, bias,
+                           bias_dtype, out, out_dtype, rows);
+    else
+        hipLaunchKernelGGL((k_gemv_narrow<M, false>), dim3(rows), dim3(kNarrowThreads), 0, s, w, cols, x, x_dtype,
+                           bias, bias_dtype, out, out_dtype, rows);
+}
+
 }  // namespace
 
 extern "C" int dmx_abi_version(void) { return DMX_ABI_VERSION; }
@@ -1891,4 +2003,27 @@ extern "C" int dmx_radix_gemv_group(const dmx_radix_tensor* const* tensors, uint
             return 1;
     }
     return 0;
+}
+
+extern "C" int dmx_gemv_narrow(const uint16_t* w, uint32_t rows, uint32_t cols, const void* x, int x_dtype,
+                               uint32_t m, const void* bias, int bias_dtype, void* out, int out_dtype, void* stream,
+                               char* err, size_t errn) {
+    if (!w) return fail(err, errn, "null weight");
+    if (rows == 0 || cols == 0) return fail(err, errn, "empty weight");
+    if (rows >= (1u << 31)) return fail(err, errn, "too many rows");
+    if (check_gemv_args(x, x_dtype, m, bias, bias_dtype, out, out_dtype, err, errn)) return 1;
+    const bool vec = cols % 8 == 0 && (reinterpret_cast<uintptr_t>(w) & 15u) == 0 &&
+                     (reinterpret_cast<uintptr_t>(x) & 15u) == 0;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    switch (m) {
+        case 1: launch_narrow_m<1>(vec, w, rows, cols, x, x_dtype, bias, bias_dtype, out, out_dtype, s); break;
+        case 2: launch_narrow_m<2>(vec, w, rows, cols, x, x_dtype, bias, bias_dtype, out, out_dtype, s); break;
+        case 3: launch_narrow_m<3>(vec, w, rows, cols, x, x_dtype, bias, bias_dtype, out, out_dtype, s); break;
+        case 4: launch_narrow_m<4>(vec, w, rows, cols, x, x_dtype, bias, bias_dtype, out, out_dtype, s); break;
+        case 5: launch_narrow_m<5>(vec, w, rows, cols, x, x_dtype, bias, bias_dtype, out, out_dtype, s); break;
+        case 6: launch_narrow_m<6>(vec, w, rows, cols, x, x_dtype, bias, bias_dtype, out, out_dtype, s); break;
+        case 7: launch_narrow_m<7>(vec, w, rows, cols, x, x_dtype, bias, bias_dtype, out, out_dtype, s); break;
+        default: launch_narrow_m<8>(vec, w, rows, cols, x, x_dtype, bias, bias_dtype, out, out_dtype, s); break;
+    }
+    return launch_check(err, errn, "narrow gemv launch");
 }

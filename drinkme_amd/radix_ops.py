@@ -8,13 +8,17 @@ module instead.
   gemv_mc(p, x)                      x [M, C], 1 <= M <= 8 -> fp32 [M, R]
   gemv_rows(p, x, bias, out_dtype)   x [M, C] -> [M, R], bias and one rounding
                                      fused (the mc arm plus swap's epilogue)
+  gemv_narrow(w, x, bias, ...)       raw bf16 w [R, C], x [M, C] -> [M, R] in x's dtype
   decode_bits(p)                     -> u16 [R, C], the source bit patterns
   decode_weight(p)                   -> bf16 [R, C]
   prepare_schedule(...)              -> u16 [nblocks], the gulp stream lengths
   read_bytes(p)                      bytes one call streams
 
-`p` is a runtime dict from swap.to_device_radix. Every call launches on
-torch's current stream and allocates only its output, with torch.
+`p` is a runtime dict from swap.to_device_radix, or a twin dict (codec
+"twin", swap.to_device_twin's: the raw bf16 `weight` [R, C]), which the
+GEMV calls run through the raw kernel (drinkme's RAW=True route,
+radix_ops.py:252-255). Every call launches on torch's current stream and
+allocates only its output, with torch.
 """
 
 from __future__ import annotations
@@ -61,27 +65,60 @@ def _dtype_code(dtype, what):
     return _DTYPE[dtype]
 
 
+def _is_twin(p: dict) -> bool:
+    """A twin dict: the raw bf16 weight, run by the raw kernel
+    (radix_ops.py:252-255)."""
+    return p.get("codec") == "twin"
+
+
+def _check_rows(x, C, device, bias, R, what):
+    if x.dim() != 2 or x.shape[1] != C:
+        raise ValueError(f"{what}: x must be [M, {C}], got {tuple(x.shape)}")
+    M = x.shape[0]
+    if not 1 <= M <= MC_MAX:
+        raise ValueError(f"{what}: M={M} outside 1..{MC_MAX}")
+    if x.device != device:
+        raise ValueError(f"{what}: x is not on the weight's device")
+    if bias is not None and (bias.numel() != R or bias.device != x.device):
+        raise ValueError(f"{what}: bias must hold R elements on the weight's device")
+    return M
+
+
+def _raw_rows(w: torch.Tensor, x: torch.Tensor, bias, out_dtype, what: str) -> torch.Tensor:
+    """The raw bf16 GEMV (dmx_gemv_narrow): w [R, C] bf16, x [M, C]."""
+    if w.dim() != 2 or w.dtype != torch.bfloat16:
+        raise TypeError(f"{what}: the weight must be a 2-D bf16 tensor, got {w.dtype} {tuple(w.shape)}")
+    R, C = int(w.shape[0]), int(w.shape[1])
+    M = _check_rows(x, C, w.device, bias, R, what)
+    w, x = w.contiguous(), x.contiguous()
+    out = torch.empty((M, R), dtype=out_dtype, device=x.device)
+    xd = _dtype_code(x.dtype, "activation")
+    od = _dtype_code(out_dtype, "output")
+    bias = bias.contiguous() if bias is not None else None
+    bd = _dtype_code(bias.dtype, "bias") if bias is not None else 0
+    err = _native.error_buffer()
+    st = _native.lib().dmx_gemv_narrow(w.data_ptr(), R, C, x.data_ptr(), xd, M,
+                                       bias.data_ptr() if bias is not None else None, bd, out.data_ptr(), od,
+                                       _stream(), err, len(err))
+    _native.check(st, err, "dmx_gemv_narrow")
+    return out
+
+
 def gemv_rows(p: dict, x: torch.Tensor, bias=None, out_dtype=torch.float32) -> torch.Tensor:
     """x [M, C] (bf16 or fp32, 1 <= M <= 8) -> [M, R] in out_dtype: the rows
     accumulated in fp32, the bias (bf16 or fp32, or None) added in fp32,
     one rounding."""
-    if x.dim() != 2 or x.shape[1] != int(p["C"]):
-        raise ValueError(f"radix gemv: x must be [M, {p['C']}], got {tuple(x.shape)}")
-    M = x.shape[0]
-    if not 1 <= M <= MC_MAX:
-        raise ValueError(f"radix gemv_mc: M={M} outside 1..{MC_MAX}")
-    if x.device != p["rx_data"].device:
-        raise ValueError("radix gemv: x is not on the weight's device")
-    x = x.contiguous()
+    if _is_twin(p):
+        return _raw_rows(p["weight"], x, bias, out_dtype, "raw gemv")
     R = int(p["R"])
+    M = _check_rows(x, int(p["C"]), p["rx_data"].device, bias, R, "radix gemv")
+    x = x.contiguous()
     out = torch.empty((M, R), dtype=out_dtype, device=x.device)
     xd = _dtype_code(x.dtype, "activation")
     od = _dtype_code(out_dtype, "output")
     if bias is not None:
         bias = bias.contiguous()
         bd = _dtype_code(bias.dtype, "bias")
-        if bias.numel() != R or bias.device != x.device:
-            raise ValueError("radix gemv: bias must hold R elements on the weight's device")
     else:
         bd = 0
     err = _native.error_buffer()
@@ -90,6 +127,17 @@ def gemv_rows(p: dict, x: torch.Tensor, bias=None, out_dtype=torch.float32) -> t
                                        _stream(), err, len(err))
     _native.check(st, err, "dmx_radix_gemv")
     return out
+
+
+def gemv_narrow(w: torch.Tensor, x: torch.Tensor, bias, block: int = 512, num_warps: int = 4) -> torch.Tensor:
+    """swap.NarrowLinear's forward for 1 <= M <= 8 rows (radix_ops.py:
+    401-415): x [M, C] (bf16 or fp32) against the row-major bf16 weight
+    w [R, C] -> [M, R] in x's dtype, the bias (if any) added in fp32 before
+    the one rounding. Raises ValueError for M outside 1..8. `block` and
+    `num_warps` are accepted for the signature and ignored: the launch
+    shape is the library's."""
+    del block, num_warps
+    return _raw_rows(w, x, bias, x.dtype, "gemv_narrow")
 
 
 def gemv_fused(p: dict, x: torch.Tensor, bias, out_dtype=torch.bfloat16) -> torch.Tensor:
@@ -125,6 +173,9 @@ def gemv_group(ps, x: torch.Tensor, biases=None, out_dtype=torch.bfloat16) -> li
     M = x.shape[0]
     if not 1 <= M <= MC_MAX:
         raise ValueError(f"radix gemv_group: M={M} outside 1..{MC_MAX}")
+    if any(_is_twin(p) for p in ps):  # raw weights: one launch each
+        bl = list(biases) if biases is not None else [None] * len(ps)
+        return [gemv_rows(p, x, b, out_dtype) for p, b in zip(ps, bl)]
     if any(x.device != p["rx_data"].device for p in ps):
         raise ValueError("radix gemv_group: x is not on the weights' device")
     x = x.contiguous()
@@ -203,7 +254,10 @@ def prepare_schedule(data, offsets, C: int, widths, B: int, nblocks: int) -> tor
 
 def read_bytes(p: dict) -> int:
     """Bytes one GEMV call streams: the payload (NW words, not the pad),
-    the directory, the tables and the schedule (radix_ops.py:435-441)."""
+    the directory, the tables and the schedule (radix_ops.py:435-441); a
+    twin's raw weight."""
+    if _is_twin(p):
+        return p["weight"].numel() * p["weight"].element_size()
     words = int(p["NW"]) if "NW" in p else p["rx_data"].numel()
     return words * 4 + sum(p[k].numel() * p[k].element_size() for k in ("rx_offsets", "rx_palette", "rx_schedule"))
 

@@ -11,6 +11,12 @@ Routes (src/drinkme/codec/swap.py:302-335):
   M > 8, dense
   disabled        "loop"   one M = 1 GEMV per row
 There is no CPU route: the arms run on the GPU and a CPU tensor is refused.
+
+Beside it, the raw bf16 surface that binds the same ops module:
+NarrowLinear / install_narrow (src/drinkme/codec/swap.py:530-627), the
+Linears under the codec's row threshold, through radix_ops.gemv_narrow;
+and to_device_twin (swap.py:168-196), a raw bf16 weight's dict that the
+GEMV calls run through the raw kernel.
 """
 
 from __future__ import annotations
@@ -158,3 +164,80 @@ def make_module(pack: dict, bias=None, device="cuda") -> torch.nn.Module:
     if pack.get("codec") != "radix":
         raise ValueError("make_module: not a radix tensor dict")
     return RadixCompressedLinear(to_device_radix(pack, device), bias)
+
+
+def eligible(child) -> bool:
+    """A Linear the codec takes (src/drinkme/codec/swap.py:850-854): bf16,
+    C % 4 == 0, both dims >= 1024."""
+    if not isinstance(child, torch.nn.Linear):
+        return False
+    w = child.weight.data
+    return w.dtype == torch.bfloat16 and w.shape[1] % 4 == 0 and min(w.shape) >= 1024
+
+
+class NarrowLinear(torch.nn.Linear):
+    """A raw bf16 Linear under the codec's row threshold, served by the raw
+    GEMV (src/drinkme/codec/swap.py:530-610): M <= 8 rows in one launch of
+    radix_ops.gemv_narrow (fp32 accumulate, the bias added in fp32, one
+    rounding); more rows, or a CPU tensor, is F.linear. The weight and bias
+    are the adopted Linear's own Parameters. Row m of an M-row call is the
+    one-row call bit for bit."""
+
+    BLOCK = 512  # drinkme's launch knobs, passed through (swap.py:577-578)
+    NUM_WARPS = 4
+    MAX_ROWS = 1024  # swap.py:581-582
+    MIN_COLS = 1024
+
+    @classmethod
+    def wants(cls, mod) -> bool:
+        if type(mod) is not torch.nn.Linear or eligible(mod):
+            return False
+        w = mod.weight
+        return (w.dtype == torch.bfloat16 and w.device.type == "cuda" and w.shape[0] <= cls.MAX_ROWS
+                and w.shape[1] >= cls.MIN_COLS and w.shape[1] % 4 == 0)
+
+    @classmethod
+    def adopt(cls, lin: torch.nn.Linear) -> "NarrowLinear":
+        """The same parameters under this class: no copy."""
+        new = cls(lin.in_features, lin.out_features, bias=lin.bias is not None, device="meta")
+        new.weight = lin.weight
+        new.bias = lin.bias
+        return new
+
+    def forward(self, x):
+        shape = x.shape
+        xm = x.reshape(-1, self.in_features)
+        if xm.shape[0] > radix_ops.MC_MAX or x.device.type != "cuda":
+            return torch.nn.functional.linear(x, self.weight, self.bias)
+        y = radix_ops.gemv_narrow(self.weight, xm, self.bias, self.BLOCK, self.NUM_WARPS)
+        return y.reshape(*shape[:-1], self.out_features)
+
+
+def install_narrow(model, device: str) -> list:
+    """Every raw Linear NarrowLinear.wants, adopted in place; returns the
+    (name, (R, C)) list (src/drinkme/codec/swap.py:613-627). Nothing off
+    the GPU."""
+    if not str(device).startswith("cuda"):
+        return []
+    done = []
+    for parent_name, parent in list(model.named_modules()):
+        for child_name, child in list(parent.named_children()):
+            if NarrowLinear.wants(child):
+                setattr(parent, child_name, NarrowLinear.adopt(child))
+                name = f"{parent_name}.{child_name}" if parent_name else child_name
+                done.append((name, tuple(child.weight.shape)))
+    return done
+
+
+def to_device_twin(w_bf16, widths=(3, 8), device: str = "cuda") -> dict:
+    """A raw bf16 weight [R, C] as a twin dict (src/drinkme/codec/swap.py:
+    168-196): the weight resident and row-major, codec "twin". The GEMV
+    calls of radix_ops run it through the raw kernel."""
+    w = w_bf16.detach()
+    if w.dtype != torch.bfloat16:
+        raise TypeError(f"to_device_twin: {w.dtype} is not bf16")
+    R, C = int(w.shape[0]), int(w.shape[1])
+    B = 1024
+    return {"weight": w.contiguous().to(torch.device(device)), "R": R, "C": C,
+            "widths": tuple(int(x) for x in widths), "block_size": B, "NBK": R * ((C + B - 1) // B),
+            "codec": "twin", "layout": 0}

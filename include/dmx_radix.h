@@ -138,6 +138,22 @@ int dmx_radix_gemv_group(const dmx_radix_tensor* const* tensors, uint32_t n, con
                          const void* const* bias, int bias_dtype, void* const* out, int out_dtype, void* stream,
                          char* err, size_t errn);
 
+/* Replaces radix_ops.gemv_narrow (src/drinkme/codec/radix_ops.py:401-415),
+ * the _gemv_narrow kernel (radix_ops.py:177-249) that swap.NarrowLinear
+ * runs (src/drinkme/codec/swap.py:530-610), and the raw (twin) GEMV of
+ * gemv_fused over a bf16 weight (radix_ops.py:252-255, stock_linear
+ * swap.py:681-707): a raw bf16 weight, no codec.
+ *   w     device [rows, cols] bf16 bits, row-major;
+ *   x     device [m, cols], x_dtype DMX_BF16 or DMX_F32, row stride cols;
+ *   m     1..8;
+ *   bias  device [rows] of bias_dtype, or NULL;
+ *   out   device [m, rows] of out_dtype.
+ * out = (x . w^T accumulated in fp32, + bias in fp32) rounded once. Row j
+ * of an m-row call equals the one-row call on x's row j bit for bit, and a
+ * bf16 x gives the same sums as its fp32 copy. */
+int dmx_gemv_narrow(const uint16_t* w, uint32_t rows, uint32_t cols, const void* x, int x_dtype, uint32_t m,
+                    const void* bias, int bias_dtype, void* out, int out_dtype, void* stream, char* err, size_t errn);
+
 /* Kernel choice for dmx_radix_gemv: DMX_POLICY_AUTO or DMX_POLICY_GENERIC
  * (an A/B switch like DRINKME_RADIX_DECODER, radix_ops.py:286-300).
  * Returns the previous policy, or -1 for an unknown one. */
