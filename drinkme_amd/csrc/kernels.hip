@@ -868,6 +868,13 @@ __global__ __launch_bounds__(kSipThreads, (M == 8 || (PH && M == 4)) ? 3 : 6) vo
         const uint32_t a0 = E0.x & 0x78u, a1 = E1.x & 0x78u, a2 = E2.x & 0x78u, a3 = E3.x & 0x78u;
         const uint32_t q1_ = __builtin_popcount(a0), q2_ = q1_ + __builtin_popcount(a1);
         const uint32_t q3_ = q2_ + __builtin_popcount(a2), cnt = q3_ + __builtin_popcount(a3);
+        // the groups' selectors depend only on the lane's own counts: read
+        // them before the scan, so their LDS round trip overlaps the
+        // cross-lane reads' (a lane with up to 16 escapes indexes rows up
+        // to 12 of sel2)
+        const uint2 sl0 = sel2[a0 >> 3], sl1 = sel2[(q1_ << 4) | (a1 >> 3)];
+        const uint2 sl2 = sel2[(q2_ << 4) | (a2 >> 3)], sl3 = sel2[(q3_ << 4) | (a3 >> 3)];
+        __builtin_amdgcn_sched_barrier(0);
         const uint32_t q0 = wave_scan_incl(cnt) - cnt;
         // the terminal is read only when the directory gives the block words
         // past its fixed streams (radix_kernel_gpu.py:96-98); without it the
@@ -883,17 +890,15 @@ __global__ __launch_bounds__(kSipThreads, (M == 8 || (PH && M == 4)) ? 3 : 6) vo
         const uint32_t w2 = __builtin_amdgcn_ds_bpermute(k0 + 8, tw);
         const uint32_t wlo = __builtin_amdgcn_alignbit(w1, w0, q0 << 3);
         const uint32_t whi = __builtin_amdgcn_alignbit(w2, w1, q0 << 3);
-        // (a lane with up to 16 escapes indexes rows up to 12 of sel2)
-#define DMX_PATCH2(E, a, off)                                                   \
-    {                                                                           \
-        const uint2 s = sel2[((off) << 4) | ((a) >> 3)];                        \
-        E.x |= __builtin_amdgcn_perm(whi, wlo, s.x) << 7;                       \
-        E.y |= __builtin_amdgcn_perm(whi, wlo, s.y) << 7;                       \
+#define DMX_PATCH2(E, s)                                \
+    {                                                   \
+        E.x |= __builtin_amdgcn_perm(whi, wlo, s.x) << 7; \
+        E.y |= __builtin_amdgcn_perm(whi, wlo, s.y) << 7; \
     }
-        DMX_PATCH2(E0, a0, 0)
-        DMX_PATCH2(E1, a1, q1_)
-        DMX_PATCH2(E2, a2, q2_)
-        DMX_PATCH2(E3, a3, q3_)
+        DMX_PATCH2(E0, sl0)
+        DMX_PATCH2(E1, sl1)
+        DMX_PATCH2(E2, sl2)
+        DMX_PATCH2(E3, sl3)
 #undef DMX_PATCH2
         // rare: a lane with more than 8 escapes, or more than 243 before it,
         // redoes its exponents with each group's four bytes read from the
@@ -1275,12 +1280,16 @@ __global__ __launch_bounds__(kSipThreads, (M == 8 || (PH && M == 4)) ? 3 : 6) vo
         uint2 E1 = t0tab[(T0 >> 8) & 0xFF];
         uint2 E2 = t0tab[(T0 >> 16) & 0xFF];
         uint2 E3 = t0tab[T0 >> 24];
+        // lane j's two tier-2 codes (tier-1 escapes 2j, 2j + 1, in tier-2
+        // word j / 4, the one it loaded) and their palette bytes: read now,
+        // beside the tier-0 lookups
+        const uint32_t sh2 = (lane & 3u) << 3;
+        const uint32_t ca = (s0.t2 >> sh2) & 15u, cb = (s0.t2 >> (sh2 + 4)) & 15u;
+        const uint32_t pa = pal2[ca], pb = pal2[cb];
+        // (M = 1 reads its activations late, beside the last lookups: the
+        // registers stay free through the tier passes)
         const uint16_t* xb = xs + c.cb * 1024 + 8 * lane;
         uint4 xa, xc;
-        if (M == 1) {
-            __builtin_memcpy(&xa, xb, 16);
-            __builtin_memcpy(&xc, xb + 512, 16);
-        }
         // twice the tier-0 escapes of each group, and their prefix in the lane
         const uint32_t h0 = (E0.x >> 15) & 15u, h1 = (E1.x >> 15) & 15u, h2 = (E2.x >> 15) & 15u;
         const uint32_t o1 = h0, o2 = o1 + h1, o3 = o2 + h2, cnt1 = (o3 + ((E3.x >> 15) & 15u)) >> 1;
@@ -1353,13 +1362,14 @@ __global__ __launch_bounds__(kSipThreads, (M == 8 || (PH && M == 4)) ? 3 : 6) vo
             E1 = make_uint2(__builtin_amdgcn_perm(0u, eb1, 0x0C010C00u) << 7, __builtin_amdgcn_perm(0u, eb1, 0x0C030C02u) << 7);
             E2 = make_uint2(__builtin_amdgcn_perm(0u, eb2, 0x0C010C00u) << 7, __builtin_amdgcn_perm(0u, eb2, 0x0C030C02u) << 7);
             E3 = make_uint2(__builtin_amdgcn_perm(0u, eb3, 0x0C010C00u) << 7, __builtin_amdgcn_perm(0u, eb3, 0x0C030C02u) << 7);
+            if (M == 1) {
+                __builtin_memcpy(&xa, xb, 16);
+                __builtin_memcpy(&xc, xb + 512, 16);
+            }
         } else {
-            // lane j resolves tier-1 escapes 2j, 2j + 1: their 4-bit codes sit in
-            // tier-2 word j / 4 (the one this lane loaded), code 15 escaping to
-            // the terminal
-            const uint32_t sh2 = (lane & 3u) << 3;
-            const uint32_t ca = (s0.t2 >> sh2) & 15u, cb = (s0.t2 >> (sh2 + 4)) & 15u;
-            uint32_t ea = pal2[ca], eb = pal2[cb];
+            // lane j resolves tier-1 escapes 2j, 2j + 1 (codes ca, cb), code 15
+            // escaping to the terminal
+            uint32_t ea = pa, eb = pb;
             const bool ta = 2 * lane < n2 && ca == 15u, tb = 2 * lane + 1 < n2 && cb == 15u;
             if (__builtin_amdgcn_ballot_w64(ta || tb) != 0 && has_term) {
                 const uint32_t nt = (uint32_t)ta + (uint32_t)tb;
@@ -1377,19 +1387,34 @@ __global__ __launch_bounds__(kSipThreads, (M == 8 || (PH && M == 4)) ? 3 : 6) vo
             // selector of (its tier-1 escapes before the group, the group's m1)
             const uint32_t kq = q1 >> 2;
             const uint32_t y0 = x2[kq], y1 = x2[kq + 1], y2 = x2[kq + 2];
+            // the groups' selectors (by their tier-1 escapes before the group
+            // and its mask m1); at M = 1 read with the activations in this
+            // round trip (at M > 1 the registers are short: read at use)
+#define DMX_SEL(P, off) sel2[((off) << 4) | ((P.x >> 3) & 15u)]
+            uint2 sg0 = {}, sg1 = {}, sg2 = {}, sg3 = {};
+            if (M == 1) {
+                sg0 = DMX_SEL(P0, 0u);
+                sg1 = DMX_SEL(P1, p1);
+                sg2 = DMX_SEL(P2, p2);
+                sg3 = DMX_SEL(P3, p3);
+                __builtin_memcpy(&xa, xb, 16);
+                __builtin_memcpy(&xc, xb + 512, 16);
+                __builtin_amdgcn_sched_barrier(0);
+            }
             const uint32_t wlo = __builtin_amdgcn_alignbit(y1, y0, (q1 & 3u) << 3);
             const uint32_t whi = __builtin_amdgcn_alignbit(y2, y1, (q1 & 3u) << 3);
-#define DMX_T2(E, P, off)                                                       \
-    {                                                                           \
-        const uint2 s = sel2[((off) << 4) | ((P.x >> 3) & 15u)];                \
-        E.x |= __builtin_amdgcn_perm(whi, wlo, s.x) << 7;                       \
-        E.y |= __builtin_amdgcn_perm(whi, wlo, s.y) << 7;                       \
+#define DMX_T2(E, sv)                                     \
+    {                                                     \
+        const uint2 s = sv;                               \
+        E.x |= __builtin_amdgcn_perm(whi, wlo, s.x) << 7; \
+        E.y |= __builtin_amdgcn_perm(whi, wlo, s.y) << 7; \
     }
-            DMX_T2(E0, P0, 0u)
-            DMX_T2(E1, P1, p1)
-            DMX_T2(E2, P2, p2)
-            DMX_T2(E3, P3, p3)
+            DMX_T2(E0, M == 1 ? sg0 : DMX_SEL(P0, 0u))
+            DMX_T2(E1, M == 1 ? sg1 : DMX_SEL(P1, p1))
+            DMX_T2(E2, M == 1 ? sg2 : DMX_SEL(P2, p2))
+            DMX_T2(E3, M == 1 ? sg3 : DMX_SEL(P3, p3))
 #undef DMX_T2
+#undef DMX_SEL
             __builtin_amdgcn_wave_barrier();
         }
         const uint32_t L0 = s0.lit.x, L1 = s0.lit.y, L2 = s0.lit.z, L3 = s0.lit.w;
