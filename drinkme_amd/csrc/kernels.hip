@@ -76,6 +76,31 @@ __device__ __forceinline__ uint32_t wave_scan_incl(uint32_t v) {
     return v;
 }
 
+// The same scan as six fused v_add_u32_dpp, written out: where the compiler
+// keeps the zero of update_dpp in a register it no longer fuses the adds
+// (twelve instructions and six register copies instead of six). A disabled
+// row is not written, which adds 0; an out-of-row source reads 0
+// (bound_ctrl). Two wait states before each DPP read of a VGPR written by
+// the VALU just before it, and after the last write.
+__device__ __forceinline__ uint32_t wave_scan_incl_dpp(uint32_t v) {
+    asm volatile(
+        "s_nop 1\n\t"
+        "v_add_u32_dpp %0, %0, %0 row_shr:1 row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
+        "s_nop 1\n\t"
+        "v_add_u32_dpp %0, %0, %0 row_shr:2 row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
+        "s_nop 1\n\t"
+        "v_add_u32_dpp %0, %0, %0 row_shr:4 row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
+        "s_nop 1\n\t"
+        "v_add_u32_dpp %0, %0, %0 row_shr:8 row_mask:0xf bank_mask:0xf bound_ctrl:1\n\t"
+        "s_nop 1\n\t"
+        "v_add_u32_dpp %0, %0, %0 row_bcast:15 row_mask:0xa bank_mask:0xf\n\t"
+        "s_nop 1\n\t"
+        "v_add_u32_dpp %0, %0, %0 row_bcast:31 row_mask:0xc bank_mask:0xf\n\t"
+        "s_nop 1"
+        : "+v"(v));
+    return v;
+}
+
 // Sum over the 64 lanes (a fixed tree: deterministic).
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
@@ -1293,7 +1318,7 @@ __global__ __launch_bounds__(kSipThreads, (M == 8 || (PH && M == 4)) ? 3 : 6) vo
         // twice the tier-0 escapes of each group, and their prefix in the lane
         const uint32_t h0 = (E0.x >> 15) & 15u, h1 = (E1.x >> 15) & 15u, h2 = (E2.x >> 15) & 15u;
         const uint32_t o1 = h0, o2 = o1 + h1, o3 = o2 + h2, cnt1 = (o3 + ((E3.x >> 15) & 15u)) >> 1;
-        const uint32_t q0 = wave_scan_incl(cnt1) - cnt1;
+        const uint32_t q0 = wave_scan_incl_dpp(cnt1) - cnt1;
         // tier 1: the lane's codes, 2 bits each from bit 2 q0 of the stream
         const int k1 = (int)((q0 >> 2) & ~3u);
         const uint32_t v0 = __builtin_amdgcn_ds_bpermute(k1, s0.t1);
