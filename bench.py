@@ -195,7 +195,8 @@ def main() -> int:
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU; --gpus {args.gpus} is not supported (this build measures one "
-              "GPU's share: the kernel is row-parallel and would shard by rows, see DESIGN.md)", file=sys.stderr)
+              "GPU's share: the kernel is row-parallel, and a multi-GPU run would give each GPU its rows)",
+              file=sys.stderr)
         return 2
 
     import torch

@@ -35,6 +35,26 @@ class RadixTensor(ct.Structure):
     ]
 
 
+class PackInfo(ct.Structure):
+    """dmx_pack_info."""
+    _fields_ = [
+        ("codec", ct.c_uint32),
+        ("block_size", ct.c_uint32),
+        ("rows", ct.c_uint64),
+        ("cols", ct.c_uint64),
+        ("n_widths", ct.c_uint32),
+        ("widths", ct.c_uint32 * 8),
+        ("profile", ct.c_char * 16),
+        ("bpw", ct.c_double),
+        ("palette_len", ct.c_uint64),
+        ("offsets_len", ct.c_uint64),
+        ("data_len", ct.c_uint64),
+    ]
+
+
+DMX_CODEC_RADIX = 0
+DMX_CODEC_RAW = 1
+
 # every symbol include/dmx_radix.h declares, with its ctypes signature
 _P, _U64, _U32, _I, _SZ = ct.c_void_p, ct.c_uint64, ct.c_uint32, ct.c_int, ct.c_size_t
 _TP = ct.POINTER(RadixTensor)
@@ -49,6 +69,8 @@ SIGNATURES = {
     "dmx_radix_gemv": (_I, [_TP, _P, _I, _U32, _P, _I, _P, _I, _P, _P, _SZ]),
     "dmx_radix_gemv_group": (_I, [_P, _U32, _P, _I, _U32, _P, _I, _P, _I, _P, _P, _SZ]),
     "dmx_gemv_narrow": (_I, [_P, _U32, _U32, _P, _I, _U32, _P, _I, _P, _I, _P, _P, _SZ]),
+    "dmx_pack_read": (_I, [ct.c_char_p, ct.c_char_p, _P, _P, _P, _P, _P, _P, _SZ]),
+    "dmx_pack_write": (_I, [ct.c_char_p, _P, _P, _P, _P, _P, _P, _SZ]),
     "dmx_radix_set_policy": (_I, [_I]),
     "dmx_synth_bf16": (_I, [_U64, _U64, _U64, ct.c_double, _U32, _P, _P, _SZ]),
 }

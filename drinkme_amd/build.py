@@ -2,11 +2,13 @@
 
     python -m drinkme_amd.build
 
-The host codec (csrc/codec.cpp) is compiled with g++, the kernels
-(csrc/kernels.hip) with hipcc for gfx950 only, and both linked into one
-shared library that ctypes loads (drinkme_amd/_native.py). Packed-fp32
-instructions are disabled for the device code (-packed-fp32-ops): hipcc
-otherwise forms v_pk_*_f32 from scalar float code.
+The host codec (csrc/codec.cpp) and the pack-file reader and writer
+(csrc/pack_io.cpp) are compiled with g++, the kernels (csrc/kernels.hip)
+with hipcc for gfx950 only, and all linked into one shared library that
+ctypes loads (drinkme_amd/_native.py). Packed-fp32 instructions are
+disabled for the device code (-packed-fp32-ops): hipcc otherwise forms
+v_pk_*_f32 from scalar float code. The host-only command line tool
+lib/dmx_pack (csrc/dmx_pack.cpp) is linked from the same host sources.
 """
 
 from __future__ import annotations
@@ -22,6 +24,7 @@ CSRC = os.path.join(HERE, "csrc")
 OBJ = os.path.join(HERE, "_build")
 LIBDIR = os.path.join(HERE, "lib")
 LIB = os.path.join(LIBDIR, "libdmx_radix.so")
+CLI = os.path.join(LIBDIR, "dmx_pack")
 INCLUDE = os.path.join(ROOT, "include")
 ARCH = "gfx950"
 
@@ -52,14 +55,20 @@ def build(verbose: bool = False) -> str:
     os.makedirs(OBJ, exist_ok=True)
     os.makedirs(LIBDIR, exist_ok=True)
     hipcc = _hipcc()
-    codec_o = os.path.join(OBJ, "codec.o")
+    host = ["g++", "-O3", "-std=c++17", "-fPIC", "-Wall", "-Wextra", "-Werror", "-pthread", f"-I{INCLUDE}"]
+    objs = []
+    for src in ("codec", "pack_io", "dmx_pack"):
+        obj = os.path.join(OBJ, f"{src}.o")
+        _run([*host, "-c", os.path.join(CSRC, f"{src}.cpp"), "-o", obj], verbose)
+        objs.append(obj)
     kern_o = os.path.join(OBJ, "kernels.o")
-    _run(["g++", "-O3", "-std=c++17", "-fPIC", "-Wall", "-Wextra", "-Werror", "-pthread", f"-I{INCLUDE}",
-          "-c", os.path.join(CSRC, "codec.cpp"), "-o", codec_o], verbose)
     _run([hipcc, *device_flags(), "-c", os.path.join(CSRC, "kernels.hip"), "-o", kern_o], verbose)
     tmp = LIB + ".tmp"
-    _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-pthread", codec_o, kern_o, "-o", tmp], verbose)
+    _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-pthread", objs[0], objs[1], kern_o, "-o", tmp],
+         verbose)
     os.replace(tmp, LIB)
+    _run(["g++", "-pthread", *objs, "-o", CLI + ".tmp"], verbose)
+    os.replace(CLI + ".tmp", CLI)
     return LIB
 
 

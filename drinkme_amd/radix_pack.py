@@ -191,10 +191,10 @@ def padded_palette_words(palette: np.ndarray, widths) -> np.ndarray:
 
 def validate_radix(p: dict) -> None:
     """The descriptor gate before any device allocation: widths, block size,
-    palette (unique entries), and the directory — monotone from 0 to the
-    payload end, every block between its fixed streams and the widest
-    block (src/drinkme/codec/radix.py:174-238; the served line of
-    src/drinkme/codec/pack.py:242-257). Raises ValueError."""
+    palette (unique entries), and the directory — strictly increasing from
+    0 to the payload end, every block between its fixed streams and the
+    widest block — with radix.validate's checks in its order and words
+    (src/drinkme/codec/radix.py:174-238). Raises ValueError."""
     widths = tuple(int(w) for w in p["widths"])
     if (len(widths) < 2 or len(widths) > 8 or widths[-1] != EXP or any(w < 1 or w > 8 for w in widths)):
         raise ValueError("radix needs 2..8 widths in 1..8, ending with the exponent width")
@@ -208,21 +208,30 @@ def validate_radix(p: dict) -> None:
     if R <= 0 or C <= 0:
         raise ValueError("invalid radix shape")
     palette = np.asarray(p["rx_palette"])
-    if palette.ndim != 1 or palette.dtype != np.uint8 or palette.size != covered or \
-            np.unique(palette).size != covered:
-        raise ValueError("invalid radix palette entries")
+    if palette.ndim != 1 or palette.dtype != np.uint8:
+        raise ValueError("invalid radix palette")
     offsets = np.asarray(p["rx_offsets"])
+    if offsets.ndim != 1 or offsets.dtype != np.uint32:
+        raise ValueError("invalid radix directory")
+    if palette.size != covered or np.unique(palette).size != covered:
+        raise ValueError("invalid radix palette entries")
     data = np.asarray(p["rx_data"])
-    if data.ndim != 1 or data.dtype != np.uint32 or offsets.ndim != 1 or offsets.dtype != np.uint32:
+    if data.ndim != 1 or data.dtype != np.uint32:
         raise ValueError("invalid radix payload")
     per_row = -(-C // B)
-    if offsets.size != R * per_row + 1 or offsets[0] != 0 or int(offsets[-1]) != data.size:
+    if (offsets.size != R * per_row + 1 or offsets[0] != 0 or int(offsets[-1]) != data.size
+            or np.any(offsets[1:] <= offsets[:-1])):
         raise ValueError("invalid radix block offsets")
     extent = np.diff(offsets.astype(np.int64))
     n = np.minimum(B, C - (np.arange(R * per_row, dtype=np.int64) % per_row) * B)
     fewest, most = block_word_bounds(n, widths)
-    bad = np.flatnonzero((extent < fewest) | (extent > most))
-    if bad.size:
-        i = int(bad[0])
-        raise ValueError(f"invalid radix block offsets: block {i} holds {int(extent[i])} words, outside "
-                         f"{int(fewest[i])}..{int(most[i])} for {int(n[i])} weights")
+    short = np.flatnonzero(extent < fewest)
+    if short.size:
+        i = int(short[0])
+        raise ValueError(f"invalid radix block offsets: block {i} holds {int(extent[i])} word(s), fewer than the "
+                         f"{int(fewest[i])} its literal plane and first tier take for {int(n[i])} weights")
+    long = np.flatnonzero(extent > most)
+    if long.size:
+        i = int(long[0])
+        raise ValueError(f"invalid radix block offsets: block {i} holds {int(extent[i])} words, more than the "
+                         f"{int(most[i])} any block of {int(n[i])} weights can use")

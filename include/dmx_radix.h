@@ -154,6 +154,43 @@ int dmx_radix_gemv_group(const dmx_radix_tensor* const* tensors, uint32_t n, con
 int dmx_gemv_narrow(const uint16_t* w, uint32_t rows, uint32_t cols, const void* x, int x_dtype, uint32_t m,
                     const void* bias, int bias_dtype, void* out, int out_dtype, void* stream, char* err, size_t errn);
 
+/* One tensor file of a drinkme pack (.npz: stored .npy members and a
+ * `scalars` JSON blob; src/drinkme/codec/pack.py:509-520, :629-644). */
+#define DMX_CODEC_RADIX 0 /* codec "radix": rx_palette, rx_offsets, rx_data */
+#define DMX_CODEC_RAW 1   /* codec "raw": raw_bits */
+
+typedef struct dmx_pack_info {
+    uint32_t codec;       /* DMX_CODEC_RADIX or DMX_CODEC_RAW */
+    uint32_t block_size;  /* radix: 1024 */
+    uint64_t rows, cols;  /* R, C */
+    uint32_t n_widths;    /* radix: tier count */
+    uint32_t widths[8];
+    char profile[16];     /* radix: "sip", "balanced" or "gulp" */
+    double bpw;           /* the scalars' bpw */
+    uint64_t palette_len; /* rx_palette entries (u8) */
+    uint64_t offsets_len; /* rx_offsets entries (u32) */
+    uint64_t data_len;    /* rx_data entries (u32) */
+} dmx_pack_info;
+
+/* Replaces pack._read_tensor (src/drinkme/codec/pack.py:629-644) for one
+ * tensor file, without NumPy: the codec named by the scalars (:119-145),
+ * R and C and the allocation cap off the ZIP directory (:164-207), then the
+ * descriptor gate (validate_tensor :210-276 over radix.validate,
+ * src/drinkme/codec/radix.py:174-238), each refusal in drinkme's words,
+ * prefixed "pack tensor <name> (<codec>): ". Fills *info; then copies each
+ * array whose buffer is non-NULL (host memory, sized from a first call
+ * with NULL buffers: palette_len bytes, offsets_len and data_len words,
+ * rows * cols u16 of raw_bits). Host threads: none. */
+int dmx_pack_read(const char* path, const char* name, dmx_pack_info* info, uint8_t* palette, uint32_t* offsets,
+                  uint32_t* data, uint16_t* raw_bits, char* err, size_t errn);
+
+/* Replaces PackWriter.add's np.savez of one tensor (pack.py:509-520): a
+ * ZIP of stored .npy members (ZIP64 where a member needs it) and the
+ * scalars as json.dumps writes them, so np.load gives back the same arrays
+ * and scalars string. Written to `path`.tmp, then renamed. */
+int dmx_pack_write(const char* path, const dmx_pack_info* info, const uint8_t* palette, const uint32_t* offsets,
+                   const uint32_t* data, const uint16_t* raw_bits, char* err, size_t errn);
+
 /* Kernel choice for dmx_radix_gemv: DMX_POLICY_AUTO or DMX_POLICY_GENERIC
  * (an A/B switch like DRINKME_RADIX_DECODER, radix_ops.py:286-300).
  * Returns the previous policy, or -1 for an unknown one. */

@@ -132,11 +132,12 @@ def test_validate_radix_refuses_blocks_outside_their_bounds(rp):
     d = _dict(rp, np.full((4, 1024), 0x3F80, np.uint16))
     off = d["rx_offsets"].copy()
     off[1] = 1
-    with pytest.raises(ValueError, match="block 0 holds 1 words, outside 320..768"):
+    with pytest.raises(ValueError, match=r"block 0 holds 1 word\(s\), fewer than the 320 its literal plane and "
+                                         r"first tier take for 1024 weights"):
         rp.validate_radix(dict(d, rx_offsets=off))
     grown = d["rx_offsets"].astype(np.int64)
     grown[1:] += 500
-    with pytest.raises(ValueError, match="outside 320..768"):
+    with pytest.raises(ValueError, match="holds 820 words, more than the 768 any block of 1024 weights can use"):
         rp.validate_radix(dict(d, rx_offsets=grown.astype(np.uint32),
                                rx_data=np.zeros(int(grown[-1]), np.uint32)))
 
