@@ -488,6 +488,7 @@ struct SipShape {
     uint32_t phase_units;     // T * psegs units per phase
     uint32_t dp, dr, ds;      // a wave's step of W units in a full tile: phases, rows, segments
     uint32_t tbl2_lds;        // dynamic-LDS byte offset of the second table; 0 = no workgroup spans two tensors
+    uint32_t young_from;      // first workgroup dispatched as a CU's second (~0u: one per CU)
     uint32_t m;               // activation rows (<= the kernel's M; rows past m are padding)
     int bias_dtype, out_dtype;
 };
@@ -1500,8 +1501,23 @@ __global__ __launch_bounds__(kSipThreads, (M == 8 || (PH && M == 4)) ? 3 : 6) vo
     };
     const uint32_t my_units = wv < units ? (units - wv + W - 1) / W : 0;
     const uint32_t items = my_units * sh.seg_blocks;
+    // Two workgroups share each SIMD, and its arbiter issues for the older
+    // one's waves first: alone, the first workgroup finishes well before
+    // the second, which then runs its last blocks without the other's
+    // waves to hide its decode latency. The second one's waves issue at a
+    // raised priority for their first three quarters of blocks, so both
+    // finish nearer together (measured 2.5-3.4% faster on Qwen3-8B layers,
+    // 1.4% on the 32B-class). sip streams near the read wall either way
+    // and keeps the default.
+    bool young = blockIdx.x >= sh.young_from;
+    const uint32_t young_end = items - items / 4;
+    if (young) __builtin_amdgcn_s_setprio(3);
     uint32_t k = 0;
     for (; k + 3 <= items; k += 3) {
+        if (young && k >= young_end) {
+            __builtin_amdgcn_s_setprio(0);
+            young = false;
+        }
         sC = gulp_load(rsrc, base, oC, nC, ln);
         uint2 oN = next_offsets();
         uint32_t nN = ns;
@@ -1771,6 +1787,9 @@ bool plan_launch(SipShape& sh, const SipGroup& g, uint32_t n, uint32_t min_rows,
                 sh.dr = rem / ps;
                 sh.ds = rem - sh.dr * ps;
                 sh.tbl2_lds = two ? (uint32_t)head : 0u;
+                // the dispatcher gives each CU one of the first cu_count
+                // workgroups, then a second from the rest
+                sh.young_from = per_cu == 2 ? (uint32_t)cu_count() : ~0u;
                 grid_out = grid;
                 lds_out = lds;
                 two_out = two;
