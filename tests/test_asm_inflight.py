@@ -1,0 +1,149 @@
+"""The sip and gulp kernels' untracked payload loads, checked on their gfx950
+assembly: no instruction between a load and its `s_waitcnt` touches the
+load's destination registers (no spill, copy or reuse of an in-flight
+register). The checker itself is pinned on small hand-written programs, each
+with one planted mistake or one pattern it must accept.
+
+Runs on the CPU: hipcc cross-compiles the device code to assembly.
+"""
+
+import os
+import shutil
+import subprocess
+
+import pytest
+
+from tests.asm_inflight import analyse, kernels
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HIPCC = "/opt/rocm/bin/hipcc"
+
+
+def _flagged(body):
+    return analyse(body)[0]
+
+
+def test_read_before_wait_is_flagged():
+    body = """
+    buffer_load_dword v1, v2, s[0:3], s4 offen
+    v_add_u32_e32 v3, v1, v1
+    s_waitcnt vmcnt(0)
+    s_endpgm
+    """
+    assert len(_flagged(body)) == 1
+
+
+def test_read_after_wait_is_clean():
+    body = """
+    buffer_load_dword v1, v2, s[0:3], s4 offen
+    s_waitcnt vmcnt(0)
+    v_add_u32_e32 v3, v1, v1
+    s_endpgm
+    """
+    assert _flagged(body) == []
+
+
+def test_partial_wait_retires_only_the_older_loads():
+    # stage A (v1, v[2:3]) then stage B (v4, v[5:6]); vmcnt(2) completes A only
+    body = """
+    buffer_load_dword v1, v10, s[0:3], s4 offen
+    buffer_load_dwordx2 v[2:3], v11, s[0:3], s4 offen
+    buffer_load_dword v4, v10, s[0:3], s5 offen
+    buffer_load_dwordx2 v[5:6], v11, s[0:3], s5 offen
+    s_waitcnt vmcnt(2)
+    v_add_u32_e32 v7, v1, v3
+    v_add_u32_e32 v8, v4, v4
+    s_waitcnt vmcnt(0)
+    s_endpgm
+    """
+    hz = _flagged(body)
+    assert len(hz) == 1 and "v8, v4, v4" in hz[0][2]
+
+
+def test_spill_and_reuse_of_an_inflight_register_are_flagged():
+    body = """
+    buffer_load_dword v1, v12, s[28:31], s18 offen
+    scratch_store_dword off, v1, off offset:32
+    v_lshrrev_b32_e32 v1, 4, v0
+    s_waitcnt vmcnt(0)
+    s_endpgm
+    """
+    assert len(_flagged(body)) == 2
+
+
+def test_a_path_that_skips_the_newer_loads_is_flagged():
+    # on the taken branch stage B is never issued, so vmcnt(2) leaves A in flight
+    body = """
+    buffer_load_dwordx2 v[2:3], v11, s[0:3], s4 offen
+    s_cmp_eq_u32 s6, 0
+    s_cbranch_scc1 .LBB0_2
+    buffer_load_dwordx2 v[5:6], v11, s[0:3], s5 offen
+.LBB0_2:
+    s_waitcnt vmcnt(2)
+    v_add_u32_e32 v7, v2, v3
+    s_waitcnt vmcnt(0)
+    s_endpgm
+    """
+    assert len(_flagged(body)) == 1
+
+
+def test_two_load_variants_of_a_uniform_branch_are_not_mixed():
+    # the compiler's form of `t ? load(b) : load(a)`: s[4:5] steers the
+    # second branch, so exactly one variant issues on every path
+    body = """
+    s_mov_b64 s[4:5], -1
+    s_and_b64 vcc, exec, s[6:7]
+    s_cbranch_vccnz .LBB0_2
+    buffer_load_dwordx2 v[2:3], v11, s[0:3], s4 offen
+    s_mov_b64 s[4:5], 0
+.LBB0_2:
+    s_andn2_b64 vcc, exec, s[4:5]
+    s_cbranch_vccnz .LBB0_4
+    buffer_load_dwordx2 v[2:3], v11, s[8:11], s4 offen
+.LBB0_4:
+    buffer_load_dwordx2 v[5:6], v11, s[0:3], s5 offen
+    s_waitcnt vmcnt(1)
+    v_add_u32_e32 v7, v2, v3
+    s_waitcnt vmcnt(0)
+    s_endpgm
+    """
+    assert _flagged(body) == []
+
+
+def test_execz_inside_a_divergent_region_keeps_both_edges():
+    # exec may be empty inside the saveexec region: the skip edge is real
+    body = """
+    buffer_load_dwordx2 v[2:3], v11, s[0:3], s4 offen
+    v_cmp_ne_u32_e32 vcc, 0, v0
+    s_and_saveexec_b64 s[6:7], vcc
+    s_cbranch_execz .LBB0_2
+    buffer_load_dwordx2 v[5:6], v11, s[0:3], s5 offen
+.LBB0_2:
+    s_or_b64 exec, exec, s[6:7]
+    s_waitcnt vmcnt(1)
+    v_add_u32_e32 v7, v2, v3
+    s_waitcnt vmcnt(0)
+    s_endpgm
+    """
+    assert len(_flagged(body)) == 1
+
+
+@pytest.fixture(scope="module")
+def kernel_asm(tmp_path_factory):
+    if not shutil.which(HIPCC) and not os.path.exists(HIPCC):
+        pytest.skip("hipcc not installed")
+    out = tmp_path_factory.mktemp("asm") / "kernels.s"
+    cmd = [HIPCC, "--offload-arch=gfx950", "-O3", "-std=c++17", "-I", os.path.join(ROOT, "include"),
+           "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "--cuda-device-only", "-S",
+           os.path.join(ROOT, "drinkme_amd", "csrc", "kernels.hip"), "-o", str(out)]
+    subprocess.run(cmd, check=True, capture_output=True, timeout=600)
+    return out.read_text()
+
+
+def test_every_sip_and_gulp_kernel_keeps_its_inflight_registers(kernel_asm):
+    ks = kernels(kernel_asm, r"k_gemv_(sip|gulp)I")
+    assert len(ks) == 20  # sip: 3 kinds x M = 1, 2, 4, 8; gulp: 2 x 4
+    for name, body in ks.items():
+        hazards, reached, total = analyse(body)
+        assert reached == total, f"{name}: walked {reached} of {total} blocks"
+        assert not hazards, f"{name}: {len(hazards)} in-flight register uses, first {hazards[0][2]!r}"
