@@ -582,6 +582,16 @@ struct SipCursor {
     uint32_t slot;      // the unit's row partial: row * S + segment
 };
 
+// What a block in flight is, taken from the cursor when its loads are
+// issued (so no second cursor walks behind the loads): its unit's row
+// partial, its column block among the resident activations, its tensor
+// among the workgroup's two, its column phase, and whether it closes its
+// unit.
+struct SipRef {
+    uint32_t slot, cb, t, p;
+    bool last;
+};
+
 // The workgroup's blocks in row-major order: [0, split_blocks) are its
 // first tensor's, from that tensor's block a_first; the rest its second
 // tensor's, from block 0. A unit lies within one row, so within one tensor.
@@ -789,10 +799,9 @@ __global__ __launch_bounds__(kSipThreads, (M == 8 || (PH && M == 4)) ? 3 : 6) vo
 
     // the first two blocks' loads go out before the tables are built; a
     // cursor past the wave's work reads the workgroup's first block instead
-    SipCursor p, c;
+    SipCursor p;
     const SipWalk wk = sip_walk(sh, nrows);
     sip_start<TWO>(sh, p, wv, wk, sp);
-    c = p;
     // each tensor's payload window: from the workgroup's first block of it
     const uint32_t base_a = ((const_u32_ptr)offsets_a)[sp.a_first], base_b = ((const_u32_ptr)offsets_b)[0];
     const i32x4 rsrc_a = make_rsrc(data_a + base_a, 0x7FFFFFFFu);
@@ -801,11 +810,15 @@ __global__ __launch_bounds__(kSipThreads, (M == 8 || (PH && M == 4)) ? 3 : 6) vo
     ln.lit = 16 * lane;
     ln.t0 = 1024 + 4 * ((3 * lane) >> 1);
     ln.term = 4 * (kSipFixed + lane);
-    uint32_t nt = 0;  // the tensor of the last next_offsets() block
+    SipRef nr;  // the last next_offsets() block
     auto next_offsets = [&]() {
         const bool live = p.p < sh.phases;
-        nt = TWO && live ? p.t : 0u;
-        const uint2 o = sip_offsets(nt ? offsets_b : offsets_a, live ? p.blk : sp.a_first);
+        nr.t = TWO && live ? p.t : 0u;
+        nr.slot = p.slot;
+        nr.cb = p.cb;
+        nr.p = p.p;
+        nr.last = p.j + 1 == sh.seg_blocks;
+        const uint2 o = sip_offsets(nr.t ? offsets_b : offsets_a, live ? p.blk : sp.a_first);
         sip_next<TWO>(sh, p, wk, sp);
         return o;
     };
@@ -813,16 +826,16 @@ __global__ __launch_bounds__(kSipThreads, (M == 8 || (PH && M == 4)) ? 3 : 6) vo
         return TWO && t ? sip_load(rsrc_b, base_b, o, 1u, ln) : sip_load(rsrc_a, base_a, o, 0u, ln);
     };
     const uint2 oA = next_offsets();
-    const uint32_t tA = nt;
+    SipRef rA = nr;
     const uint2 oB = next_offsets();
-    const uint32_t tB = nt;
+    SipRef rB = nr;
     uint2 oC = next_offsets();
-    uint32_t tC = nt;
+    SipRef rC = nr;
     // the prologue's stages issue in the loop's order (no interleaving),
     // so the waits the loop needs are the same on entry as in steady state
-    SipStage sA = load(oA, tA);
+    SipStage sA = load(oA, rA.t);
     __builtin_amdgcn_sched_barrier(0);
-    SipStage sB = load(oB, tB);
+    SipStage sB = load(oB, rB.t);
     __builtin_amdgcn_sched_barrier(0);
     SipStage sC;
 
@@ -872,7 +885,7 @@ __global__ __launch_bounds__(kSipThreads, (M == 8 || (PH && M == 4)) ? 3 : 6) vo
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
     };
-    auto process = [&](const SipStage& s0) {
+    auto process = [&](const SipStage& s0, const SipRef& c) {
         if (PH)
             while (cur_phase < c.p) phase_advance();
         const uint2* tb = TWO && s0.t ? tbl2 : tbl;
@@ -991,7 +1004,7 @@ __global__ __launch_bounds__(kSipThreads, (M == 8 || (PH && M == 4)) ? 3 : 6) vo
             }
         }
 
-        if (c.j + 1 == sh.seg_blocks) {
+        if (c.last) {
             if (M == 1) {
                 const float s = wave_sum_dpp(acc0 + acc1);
                 if (lane == 0) red[c.slot] = s;
@@ -1007,7 +1020,6 @@ __global__ __launch_bounds__(kSipThreads, (M == 8 || (PH && M == 4)) ? 3 : 6) vo
                 }
             }
         }
-        sip_next<TWO>(sh, c, wk, sp);
     };
     // three stages rotate roles (no register copies); each step issues the
     // stage two blocks ahead, then completes the oldest (six loads newer);
@@ -1016,27 +1028,31 @@ __global__ __launch_bounds__(kSipThreads, (M == 8 || (PH && M == 4)) ? 3 : 6) vo
     const uint32_t items = my_units * sh.seg_blocks;
     uint32_t k = 0;
     for (; k + 3 <= items; k += 3) {
-        sC = load(oC, tC);
+        sC = load(oC, rC.t);
         uint2 oN = next_offsets();
-        uint32_t tN = nt;
+        SipRef rN = nr;
         SIP_WAIT(6, sA);
-        process(sA);
-        sA = load(oN, tN);
+        process(sA, rA);
+        sA = load(oN, rN.t);
+        rA = rN;
         oN = next_offsets();
-        tN = nt;
+        rN = nr;
         SIP_WAIT(6, sB);
-        process(sB);
-        sB = load(oN, tN);
-        oC = next_offsets();
-        tC = nt;
+        process(sB, rB);
+        sB = load(oN, rN.t);
+        rB = rN;
+        oN = next_offsets();
+        rN = nr;
         SIP_WAIT(6, sC);
-        process(sC);
+        process(sC, rC);
+        oC = oN;
+        rC = rN;
     }
     // in flight now: sA (older), then sB
     SIP_WAIT(3, sA);
-    if (k < items) process(sA);
+    if (k < items) process(sA, rA);
     SIP_WAIT(0, sB);
-    if (k + 1 < items) process(sB);
+    if (k + 1 < items) process(sB, rB);
     if (PH)
         while (cur_phase + 1 < sh.phases) phase_advance();
     __syncthreads();
