@@ -32,6 +32,7 @@
 #include <algorithm>
 #include <atomic>
 #include <cmath>
+#include <numeric>
 
 #include "dmx_radix.h"
 
@@ -1758,16 +1759,38 @@ bool sip_eligible(const dmx_radix_tensor* t, const void* x, int x_dtype, uint32_
 // block). W is the kernel's waves per workgroup, mf whether its verify rows
 // use the matrix cores (their activation rows get a padded stride), `fixed`
 // its static LDS; a second exponent table is added when a tile spans two tensors (allowed
-// only with `allow_two`). Returns false, planning nothing, when no plan
-// fits.
+// only with `allow_two`). Without it, a group whose tensor boundaries the
+// even tile would cut takes the tile height, from T/2 to 4T, that divides
+// every boundary and puts the fewest rows on the busiest CU (the
+// workgroups beyond the resident ones run as a later round). Returns false,
+// planning nothing, when no plan fits.
 bool plan_launch(SipShape& sh, const SipGroup& g, uint32_t n, uint32_t min_rows, uint32_t M, uint32_t W,
                  bool mf, size_t fixed, bool allow_two, uint32_t& grid_out, size_t& lds_out, bool& two_out) {
+    const uint32_t cus = (uint32_t)cu_count();
     for (uint32_t per_cu = M == 8 ? 1 : 2; per_cu >= 1; --per_cu) {
-        uint32_t grid = std::min<uint32_t>(sh.rows, (uint32_t)cu_count() * per_cu);
-        const uint32_t T = (sh.rows + grid - 1) / grid;
-        grid = (sh.rows + T - 1) / T;
+        uint32_t grid = std::min<uint32_t>(sh.rows, cus * per_cu);
+        uint32_t T = (sh.rows + grid - 1) / grid;
         bool two = false;
         for (uint32_t i = 1; i < n; ++i) two |= g.row0[i] % T != 0;
+        if (two && !allow_two) {
+            uint32_t gb = 0;  // the tile height must divide every boundary
+            for (uint32_t i = 1; i < n; ++i) gb = std::gcd(gb, g.row0[i]);
+            uint32_t best = 0;
+            uint64_t best_rows = ~0ull;
+            for (uint32_t t = std::max(1u, T / 2); t <= 4 * T && t <= gb; ++t) {
+                if (gb % t) continue;
+                const uint64_t busiest = ((uint64_t)(sh.rows + t - 1) / t + cus - 1) / cus * t;
+                if (busiest < best_rows || (busiest == best_rows && t > best)) {
+                    best_rows = busiest;
+                    best = t;
+                }
+            }
+            if (best) {
+                T = best;
+                two = false;
+            }
+        }
+        grid = (sh.rows + T - 1) / T;
         if (T <= min_rows && (allow_two || !two)) {
             for (uint32_t P = 1; P <= sh.nb; ++P) {
                 if (sh.nb % P) continue;

@@ -64,6 +64,37 @@ def test_group_matches_the_oracle(cuda, rows, C, M):
     assert all(torch.equal(a, b) for a, b in zip(again, ys))
 
 
+@pytest.mark.parametrize("rows,C,M", [((4096, 1024, 1024), 4096, 1), ((4096, 1024, 1024), 4096, 4),
+                                      ((8192, 1024, 1024), 5120, 1), ((12288, 12288), 4096, 1),
+                                      ((640, 128, 128), 1024, 8), ((1000, 37, 2000), 2048, 1)])
+def test_gulp_group_matches_the_oracle(cuda, rows, C, M):
+    """gulp groups: the kernel keeps one tensor per workgroup, so q/k/v-like
+    groups run as one launch with a tile height that divides every tensor
+    boundary (8 rows for 4096/1024/1024); a group with no such height
+    (1000/37/2000) runs tensor by tensor. Same bars as sip."""
+    import torch
+
+    from drinkme_amd import radix_ops, swap
+
+    rng = np.random.default_rng(zlib.crc32(repr(("gulp", rows, C, M)).encode()))
+    kinds = ("tight", "spread", "escapes")
+    bits = [_bits(rng, (r, C), kinds[i % 3]) for i, r in enumerate(rows)]
+    rts = [swap.to_device_radix(oracle_dict(b, "gulp"), cuda) for b in bits]
+    xb = O.f32_to_bf16_bits(rng.standard_normal((M, C)).astype(np.float32))
+    x = bf16_tensor(xb, cuda)
+    xf = O.bf16_bits_to_f32(xb)
+    print(f"case gulp group rows={rows} C={C} M={M}", flush=True)
+    ys = radix_ops.gemv_group(rts, x, None, torch.float32)
+    for i, (y, b) in enumerate(zip(ys, bits)):
+        _check(y.cpu().numpy(), xf, b, f"gulp group {rows} tensor {i}")
+    biases = [bf16_tensor(O.f32_to_bf16_bits(rng.standard_normal(r).astype(np.float32)), cuda) for r in rows]
+    fused = radix_ops.gemv_group(rts, x, biases, torch.bfloat16)
+    for i, (f, y) in enumerate(zip(fused, ys)):
+        assert torch.equal(f, (y + biases[i].float()).to(torch.bfloat16)), f"gulp group {rows} tensor {i}: epilogue"
+    again = radix_ops.gemv_group(rts, x, None, torch.float32)
+    assert all(torch.equal(a, b) for a, b in zip(again, ys))
+
+
 def test_group_fallbacks_match_the_oracle(cuda):
     """Groups the one-launch kernel does not take run tensor by tensor:
     more than four tensors, a tensor shorter than the row tile, a gulp
