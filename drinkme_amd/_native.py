@@ -69,6 +69,7 @@ SIGNATURES = {
     "dmx_radix_gemv": (_I, [_TP, _P, _I, _U32, _P, _I, _P, _I, _P, _P, _SZ]),
     "dmx_radix_gemv_group": (_I, [_P, _U32, _P, _I, _U32, _P, _I, _P, _I, _P, _P, _SZ]),
     "dmx_gemv_narrow": (_I, [_P, _U32, _U32, _P, _I, _U32, _P, _I, _P, _I, _P, _P, _SZ]),
+    "dmx_radix_gemv_twin": (_I, [_P, _U32, _U32, _U32, _U32, _P, _P, _I, _U32, _P, _I, _P, _I, _P, _P, _SZ]),
     "dmx_pack_read": (_I, [ct.c_char_p, ct.c_char_p, _P, _P, _P, _P, _P, _P, _SZ]),
     "dmx_pack_write": (_I, [ct.c_char_p, _P, _P, _P, _P, _P, _P, _SZ]),
     "dmx_radix_set_policy": (_I, [_I]),

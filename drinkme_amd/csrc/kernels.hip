@@ -246,7 +246,9 @@ __global__ __launch_bounds__(kGenThreads) void k_schedule(Desc d, uint16_t* __re
 // One workgroup per output row: the row's blocks decoded in turn, each
 // weight multiplied into M fp32 accumulators; the row's sums reduced over
 // the workgroup in a fixed order, the bias added in fp32, one rounding.
-template <int M>
+// RAW: the raw twin, the row-major bf16 weight at d.data read at the
+// positions the decode fills, everything else the same.
+template <int M, bool RAW = false>
 __global__ __launch_bounds__(kGenThreads) void k_gemv_generic(Desc d, const void* __restrict__ x, int x_dtype,
                                                               const void* __restrict__ bias, int bias_dtype,
                                                               void* __restrict__ out, int out_dtype) {
@@ -260,7 +262,16 @@ __global__ __launch_bounds__(kGenThreads) void k_gemv_generic(Desc d, const void
     for (uint32_t b = 0; b < d.nb; ++b) {
         const uint32_t c0 = b * d.block, n = min(d.block, d.cols - c0);
         uint32_t bits[kGenK];
-        decode_block(d, row * d.nb + b, n, K, bits, sh, nullptr);
+        if constexpr (RAW) {
+            const uint16_t* wr = reinterpret_cast<const uint16_t*>(d.data) + (uint64_t)row * d.cols + c0;
+#pragma unroll
+            for (int k = 0; k < kGenK; ++k) {
+                const uint32_t i = threadIdx.x * K + k;
+                bits[k] = (uint32_t)k < K && i < n ? wr[i] : 0u;
+            }
+        } else {
+            decode_block(d, row * d.nb + b, n, K, bits, sh, nullptr);
+        }
 #pragma unroll
         for (int k = 0; k < kGenK; ++k) {
             uint32_t i = threadIdx.x * K + k;
@@ -513,6 +524,7 @@ struct SipStage {
     uint32_t term;
     uint32_t start, end;
     uint32_t t;  // 0: the workgroup's first tensor, 1: its second
+    u32x4 hi;    // raw twin: the lane's weights 16l + 8 .. 16l + 15 (lit holds 16l .. 16l + 7)
 };
 
 // The directory, read-only for the whole launch: through the constant
@@ -529,6 +541,7 @@ __device__ __forceinline__ uint2 sip_offsets(const uint32_t* offsets, uint32_t b
 // two tier-0 words (48 bits at bit 48l) and word l of the terminal region.
 struct SipLanes {
     uint32_t lit, t0, term;
+    uint32_t raw;  // raw twin: 32 l, the lane's 16 bf16 weights of a block
 };
 
 typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
@@ -573,6 +586,23 @@ __device__ __forceinline__ SipStage sip_load(i32x4 rsrc, uint32_t base, uint2 o,
 // The "+v" operands make S's registers this statement's results, so nothing
 // reads them before the wait.
 #define SIP_WAIT(N, S) asm volatile("s_waitcnt vmcnt(" #N ")" : "+v"(S.lit), "+v"(S.t0), "+v"(S.term))
+
+// The raw twin's block: lane l's 16 bf16 weights, 32 bytes at byte offset
+// `off` of the workgroup's first row plus 32 l, as two 128-bit loads (word
+// j of the pair = weights 16l + 2j, 16l + 2j + 1: the pair words the decode
+// builds). Untracked like the payload loads: completed by RAW_WAIT.
+__device__ __forceinline__ SipStage raw_load(i32x4 rsrc, uint32_t off, const SipLanes& ln) {
+    SipStage s;
+    s.start = s.end = s.t = 0;
+    asm volatile(
+        "buffer_load_dwordx4 %0, %2, %3, %4 offen\n\t"
+        "buffer_load_dwordx4 %1, %2, %3, %4 offen offset:16"
+        : "=&v"(s.lit), "=&v"(s.hi)
+        : "v"(ln.raw), "s"(rsrc), "s"(off));
+    return s;
+}
+
+#define RAW_WAIT(N, S) asm volatile("s_waitcnt vmcnt(" #N ")" : "+v"(S.lit), "+v"(S.hi))
 
 // A wave's place in its work: block j of the unit, the block's index in its
 // tensor's directory, its column block among the resident activation
@@ -750,9 +780,10 @@ __device__ __forceinline__ void sip_table(uint2* tb, const uint32_t* palette) {
 // PH: the activation columns come in phases (sh.phases > 1), for rows too
 // long for LDS; the other instantiations carry no phase code. (With M = 4
 // too, it keeps one workgroup per CU, for the registers.)
-template <bool TWO, int M, bool PH>
+template <bool TWO, int M, bool PH, int RAW = 0>
 __global__ __launch_bounds__(kSipThreads, (M == 8 || (PH && M == 4)) ? 3 : 6) void k_gemv_sip(const SipGroup g, const uint16_t* __restrict__ x,
                                                           const SipShape sh) {
+    static_assert(!(TWO && RAW), "the raw twin runs one tensor");
     // fixed-size tables in static LDS (their addresses fold into the LDS
     // instructions' offsets); the activation, the row partials and a second
     // tensor's table after them
@@ -804,13 +835,19 @@ __global__ __launch_bounds__(kSipThreads, (M == 8 || (PH && M == 4)) ? 3 : 6) vo
     const SipWalk wk = sip_walk(sh, nrows);
     sip_start<TWO>(sh, p, wv, wk, sp);
     // each tensor's payload window: from the workgroup's first block of it
-    const uint32_t base_a = ((const_u32_ptr)offsets_a)[sp.a_first], base_b = ((const_u32_ptr)offsets_b)[0];
-    const i32x4 rsrc_a = make_rsrc(data_a + base_a, 0x7FFFFFFFu);
+    // (the raw twin: from the workgroup's first row, 512 words a block)
+    uint32_t base_a = 0, base_b = 0;
+    if constexpr (!RAW) {
+        base_a = ((const_u32_ptr)offsets_a)[sp.a_first];
+        base_b = ((const_u32_ptr)offsets_b)[0];
+    }
+    const i32x4 rsrc_a = make_rsrc(RAW ? data_a + (uint64_t)sp.a_first * 512u : data_a + base_a, 0x7FFFFFFFu);
     const i32x4 rsrc_b = make_rsrc(data_b + base_b, 0x7FFFFFFFu);
     SipLanes ln;
     ln.lit = 16 * lane;
     ln.t0 = 1024 + 4 * ((3 * lane) >> 1);
     ln.term = 4 * (kSipFixed + lane);
+    ln.raw = 32 * lane;
     SipRef nr;  // the last next_offsets() block
     auto next_offsets = [&]() {
         const bool live = p.p < sh.phases;
@@ -819,11 +856,16 @@ __global__ __launch_bounds__(kSipThreads, (M == 8 || (PH && M == 4)) ? 3 : 6) vo
         nr.cb = p.cb;
         nr.p = p.p;
         nr.last = p.j + 1 == sh.seg_blocks;
-        const uint2 o = sip_offsets(nr.t ? offsets_b : offsets_a, live ? p.blk : sp.a_first);
+        uint2 o;
+        if constexpr (RAW)  // the block's byte offset from the workgroup's first row
+            o = make_uint2(((live ? p.blk : sp.a_first) - sp.a_first) * 2048u, 0u);
+        else
+            o = sip_offsets(nr.t ? offsets_b : offsets_a, live ? p.blk : sp.a_first);
         sip_next<TWO>(sh, p, wk, sp);
         return o;
     };
     auto load = [&](uint2 o, uint32_t t) {
+        if constexpr (RAW) return raw_load(rsrc_a, o.x, ln);
         return TWO && t ? sip_load(rsrc_b, base_b, o, 1u, ln) : sip_load(rsrc_a, base_a, o, 0u, ln);
     };
     const uint2 oA = next_offsets();
@@ -840,6 +882,7 @@ __global__ __launch_bounds__(kSipThreads, (M == 8 || (PH && M == 4)) ? 3 : 6) vo
     __builtin_amdgcn_sched_barrier(0);
     SipStage sC;
 
+    if constexpr (!RAW) {
     sip_table(tbl, pick(g.palette, ia));
     if (two) sip_table(tbl2, pick(g.palette, ib));
     // selectors of escape mask m (4 weights) at offset o: byte 0 / 2 of word
@@ -856,16 +899,21 @@ __global__ __launch_bounds__(kSipThreads, (M == 8 || (PH && M == 4)) ? 3 : 6) vo
         sel2[i] = e;
         if (o == 0) sel[m] = e;
     }
+    }
     // every wave's direct loads into LDS must land before any wave reads:
-    // they precede the two stages' 6 loads in the wave's queue, so vmcnt(6)
-    // completes them while the stages stay in flight
-    asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
+    // they precede the two stages' 6 loads (raw: 4) in the wave's queue, so
+    // vmcnt(6) completes them while the stages stay in flight
+    if constexpr (RAW)
+        asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+    else
+        asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
     __syncthreads();
 
     const uint32_t keep = 0x807F807Fu;  // sign + mantissa bits of a bf16 pair, from the literal
     // M = 1 keeps two accumulator chains; M > 1 one per row
     float acc0 = 0.0f, acc1 = 0.0f;
-    constexpr bool MF = sip_mfma(M);  // verify rows on the matrix cores
+    // verify rows on the matrix cores (a raw twin mirroring gulp: gulp's rule)
+    constexpr bool MF = RAW == 2 ? gulp_mfma(M) : sip_mfma(M);
     constexpr int MA = MF ? 1 : M, MD = MF ? M : 1;
     float acc[MA];
 #pragma unroll
@@ -889,6 +937,25 @@ __global__ __launch_bounds__(kSipThreads, (M == 8 || (PH && M == 4)) ? 3 : 6) vo
     auto process = [&](const SipStage& s0, const SipRef& c) {
         if (PH)
             while (cur_phase < c.p) phase_advance();
+        const uint16_t* xb;
+        uint4 xa, xc;
+        uint32_t wp[8];
+        if constexpr (RAW) {
+            // the twin: the lane's raw pair words in place of the decode
+            xb = xs + c.cb * 1024 + 8 * lane;
+            if (M == 1) {
+                __builtin_memcpy(&xa, xb, 16);
+                __builtin_memcpy(&xc, xb + 512, 16);
+            }
+            wp[0] = s0.lit.x;
+            wp[1] = s0.lit.y;
+            wp[2] = s0.lit.z;
+            wp[3] = s0.lit.w;
+            wp[4] = s0.hi.x;
+            wp[5] = s0.hi.y;
+            wp[6] = s0.hi.z;
+            wp[7] = s0.hi.w;
+        } else {
         const uint2* tb = TWO && s0.t ? tbl2 : tbl;
         const uint64_t v = ((uint64_t)s0.t0.y << 32 | s0.t0.x) >> ((lane & 1) * 16);
         const uint32_t lo = (uint32_t)v, hi = (uint32_t)(v >> 32);
@@ -896,8 +963,7 @@ __global__ __launch_bounds__(kSipThreads, (M == 8 || (PH && M == 4)) ? 3 : 6) vo
         uint2 E1 = tb[(lo >> 12) & 0xFFF];
         uint2 E2 = tb[__builtin_amdgcn_alignbit(hi, lo, 24) & 0xFFF];
         uint2 E3 = tb[(hi >> 4) & 0xFFF];
-        const uint16_t* xb = xs + c.cb * 1024 + 8 * lane;
-        uint4 xa, xc;
+        xb = xs + c.cb * 1024 + 8 * lane;
         if (M == 1) {
             __builtin_memcpy(&xa, xb, 16);
             __builtin_memcpy(&xc, xb + 512, 16);
@@ -967,7 +1033,6 @@ __global__ __launch_bounds__(kSipThreads, (M == 8 || (PH && M == 4)) ? 3 : 6) vo
 #undef DMX_PATCH
         }
         const uint32_t L0 = s0.lit.x, L1 = s0.lit.y, L2 = s0.lit.z, L3 = s0.lit.w;
-        uint32_t wp[8];
         wp[0] = (__builtin_amdgcn_perm(L0, L0, 0x01010000) & keep) | (E0.x & ~keep);
         wp[1] = (__builtin_amdgcn_perm(L0, L0, 0x03030202) & keep) | (E0.y & ~keep);
         wp[2] = (__builtin_amdgcn_perm(L1, L1, 0x01010000) & keep) | (E1.x & ~keep);
@@ -976,6 +1041,7 @@ __global__ __launch_bounds__(kSipThreads, (M == 8 || (PH && M == 4)) ? 3 : 6) vo
         wp[5] = (__builtin_amdgcn_perm(L2, L2, 0x03030202) & keep) | (E2.y & ~keep);
         wp[6] = (__builtin_amdgcn_perm(L3, L3, 0x01010000) & keep) | (E3.x & ~keep);
         wp[7] = (__builtin_amdgcn_perm(L3, L3, 0x03030202) & keep) | (E3.y & ~keep);
+        }
         if (M == 1) {
             acc0 = dot2(wp[0], xa.x, acc0);
             acc1 = dot2(wp[1], xa.y, acc1);
@@ -1032,27 +1098,27 @@ __global__ __launch_bounds__(kSipThreads, (M == 8 || (PH && M == 4)) ? 3 : 6) vo
         sC = load(oC, rC.t);
         uint2 oN = next_offsets();
         SipRef rN = nr;
-        SIP_WAIT(6, sA);
+        if constexpr (RAW) RAW_WAIT(4, sA); else SIP_WAIT(6, sA);
         process(sA, rA);
         sA = load(oN, rN.t);
         rA = rN;
         oN = next_offsets();
         rN = nr;
-        SIP_WAIT(6, sB);
+        if constexpr (RAW) RAW_WAIT(4, sB); else SIP_WAIT(6, sB);
         process(sB, rB);
         sB = load(oN, rN.t);
         rB = rN;
         oN = next_offsets();
         rN = nr;
-        SIP_WAIT(6, sC);
+        if constexpr (RAW) RAW_WAIT(4, sC); else SIP_WAIT(6, sC);
         process(sC, rC);
         oC = oN;
         rC = rN;
     }
     // in flight now: sA (older), then sB
-    SIP_WAIT(3, sA);
+    if constexpr (RAW) RAW_WAIT(2, sA); else SIP_WAIT(3, sA);
     if (k < items) process(sA, rA);
-    SIP_WAIT(0, sB);
+    if constexpr (RAW) RAW_WAIT(0, sB); else SIP_WAIT(0, sB);
     if (k + 1 < items) process(sB, rB);
     if (PH)
         while (cur_phase + 1 < sh.phases) phase_advance();
@@ -1983,11 +2049,11 @@ int launch_gulp(const dmx_radix_tensor* const* ts, uint32_t n, const void* x, ui
     return launch_check(err, errn, "gulp gemv launch");
 }
 
-template <int M>
+template <int M, bool RAW = false>
 void launch_generic_m(const Desc& d, const void* x, int x_dtype, const void* bias, int bias_dtype, void* out,
                       int out_dtype, hipStream_t stream) {
-    hipLaunchKernelGGL(k_gemv_generic<M>, dim3(d.rows), dim3(kGenThreads), 0, stream, d, x, x_dtype, bias, bias_dtype,
-                       out, out_dtype);
+    hipLaunchKernelGGL((k_gemv_generic<M, RAW>), dim3(d.rows), dim3(kGenThreads), 0, stream, d, x, x_dtype, bias,
+                       bias_dtype, out, out_dtype);
 }
 
 int check_gemv_args(const void* x, int x_dtype, uint32_t m, const void* bias, int bias_dtype, const void* out,
@@ -2134,4 +2200,122 @@ extern "C" int dmx_gemv_narrow(const uint16_t* w, uint32_t rows, uint32_t cols, 
         default: launch_narrow_m<8>(vec, w, rows, cols, x, x_dtype, bias, bias_dtype, out, out_dtype, s); break;
     }
     return launch_check(err, errn, "narrow gemv launch");
+}
+
+// --------------------------------------------------------------- raw twin --
+
+typedef void (*RawKernel)(const SipGroup, const uint16_t*, const SipShape);
+
+// k_gemv_sip's raw instantiations: phased or not; M = 1, 2, 4, 8 (mi); at
+// M = 4 the matrix-core rule of the kernel mirrored (sip: MFMA, gulp:
+// v_dot2). At M = 1, 2 and 8 the sip and gulp kernels do the same
+// arithmetic, so one instantiation mirrors both.
+RawKernel raw_kernel(bool phased, int mi, bool gulp) {
+    static const RawKernel table[2][5] = {
+        {k_gemv_sip<false, 1, false, 1>, k_gemv_sip<false, 2, false, 1>, k_gemv_sip<false, 4, false, 1>,
+         k_gemv_sip<false, 8, false, 1>, k_gemv_sip<false, 4, false, 2>},
+        {k_gemv_sip<false, 1, true, 1>, k_gemv_sip<false, 2, true, 1>, k_gemv_sip<false, 4, true, 1>,
+         k_gemv_sip<false, 8, true, 1>, k_gemv_sip<false, 4, true, 2>}};
+    return table[phased ? 1 : 0][gulp && mi == 2 ? 4 : mi];
+}
+
+// The twin over the fast kernels' work split: the plan the mirrored kernel
+// (sip, or gulp with `gulp`) makes for a tensor of this shape (its static
+// LDS, matrix-core rule and waves), so every sum runs in that kernel's
+// order. Returns 2, having launched nothing, when that kernel would not take
+// the tensor either.
+int launch_raw(const uint16_t* w, uint32_t rows, uint32_t cols, bool gulp, const void* x, uint32_t m,
+               const void* bias, int bias_dtype, void* out, int out_dtype, hipStream_t stream, char* err,
+               size_t errn) {
+    if (m < 1 || m > 8) return 2;
+    const int mi = m == 1 ? 0 : m == 2 ? 1 : m <= 4 ? 2 : 3;
+    const uint32_t M = 1u << mi;
+    SipGroup g;
+    SipShape sh;
+    for (uint32_t i = 0; i < (uint32_t)kGroupMax; ++i) {
+        g.data[i] = reinterpret_cast<const uint32_t*>(w);
+        g.offsets[i] = nullptr;
+        g.palette[i] = nullptr;
+        g.schedule[i] = nullptr;
+        g.bias[i] = bias;
+        g.out[i] = out;
+        g.row0[i] = i == 0 ? 0u : rows;
+    }
+    g.row0[kGroupMax] = rows;
+    sh.rows = rows;
+    sh.cols = cols;
+    sh.nb = cols / 1024;
+    sh.n = 1;
+    sh.m = m;
+    sh.tbl2_lds = 0;
+    sh.bias_dtype = bias_dtype;
+    sh.out_dtype = out_dtype;
+    const size_t sip_fixed = kTableBytes + kSelBytes;
+    const size_t fixed = gulp ? kGulpT0Bytes + kTableBytes + 13 * 16 * 8 + 16 + kSipWaves * kGulpX2Words * 4 : sip_fixed;
+    uint32_t grid = 0;
+    size_t lds = 0;
+    bool two = false;
+    if (!plan_launch(sh, g, 1, rows, M, kSipWaves, gulp ? gulp_mfma((int)M) : sip_mfma((int)M), fixed, !gulp, grid,
+                     lds, two))
+        return 2;
+    if ((uint64_t)sh.rows_per_wg * cols * 2 >= (1ull << 31)) return 2;  // a tile's bytes within the buffer range
+    static std::atomic<size_t> lds_opted{64 * 1024 - sip_fixed};  // the raw kernels declare sip's static LDS
+    if (lds > lds_opted.load()) {
+        for (int t = 0; t < 2; ++t)
+            for (int i = 0; i < 5; ++i) {
+                hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(raw_kernel(t, i & 3, i == 4)),
+                                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+                if (e != hipSuccess) return fail_hip(err, errn, "raw twin kernel LDS opt-in", e);
+            }
+        lds_opted.store(lds);
+    }
+    hipLaunchKernelGGL(raw_kernel(sh.phases > 1, mi, gulp), dim3(grid), dim3(kSipThreads), lds, stream, g,
+                       static_cast<const uint16_t*>(x), sh);
+    return launch_check(err, errn, "raw twin gemv launch");
+}
+
+extern "C" int dmx_radix_gemv_twin(const uint16_t* w, uint32_t rows, uint32_t cols, uint32_t block_size,
+                                   uint32_t n_widths, const uint32_t* widths, const void* x, int x_dtype, uint32_t m,
+                                   const void* bias, int bias_dtype, void* out, int out_dtype, void* stream,
+                                   char* err, size_t errn) {
+    if (!w) return fail(err, errn, "null weight");
+    if (rows == 0 || cols == 0) return fail(err, errn, "empty weight");
+    if (block_size < 32 || block_size > 4096 || (block_size & (block_size - 1)))
+        return fail(err, errn, "block_size must be a power of two from 32 through 4096");
+    if (!widths || n_widths < 2 || n_widths > 8 || widths[n_widths - 1] != 8)
+        return fail(err, errn, "radix needs 2..8 widths in 1..8, ending with the exponent width");
+    if ((uint64_t)rows * ((cols + block_size - 1) / block_size) >= (1ull << 31)) return fail(err, errn, "too many blocks");
+    if (check_gemv_args(x, x_dtype, m, bias, bias_dtype, out, out_dtype, err, errn)) return 1;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    // the kernel the compressed tensor of these widths would run (gemv_one)
+    dmx_radix_tensor t = {};
+    t.rows = rows;
+    t.cols = cols;
+    t.block_size = block_size;
+    t.n_widths = n_widths;
+    for (uint32_t j = 0; j < n_widths; ++j) t.widths[j] = widths[j];
+    const bool fast = g_policy.load() == DMX_POLICY_AUTO && m >= 1 && m <= 8 && x_dtype == DMX_BF16 &&
+                      block_size == 1024 && cols % 1024 == 0 && (reinterpret_cast<uintptr_t>(x) & 15u) == 0 &&
+                      (reinterpret_cast<uintptr_t>(w) & 15u) == 0;
+    if (fast && (is_sip(&t) || is_gulp(&t))) {
+        const int rc = launch_raw(w, rows, cols, is_gulp(&t), x, m, bias, bias_dtype, out, out_dtype, s, err, errn);
+        if (rc != 2) return rc;
+    }
+    Desc d = {};
+    d.data = reinterpret_cast<const uint32_t*>(w);
+    d.rows = rows;
+    d.cols = cols;
+    d.block = block_size;
+    d.nb = (cols + block_size - 1) / block_size;
+    switch (m) {
+        case 1: launch_generic_m<1, true>(d, x, x_dtype, bias, bias_dtype, out, out_dtype, s); break;
+        case 2: launch_generic_m<2, true>(d, x, x_dtype, bias, bias_dtype, out, out_dtype, s); break;
+        case 3: launch_generic_m<3, true>(d, x, x_dtype, bias, bias_dtype, out, out_dtype, s); break;
+        case 4: launch_generic_m<4, true>(d, x, x_dtype, bias, bias_dtype, out, out_dtype, s); break;
+        case 5: launch_generic_m<5, true>(d, x, x_dtype, bias, bias_dtype, out, out_dtype, s); break;
+        case 6: launch_generic_m<6, true>(d, x, x_dtype, bias, bias_dtype, out, out_dtype, s); break;
+        case 7: launch_generic_m<7, true>(d, x, x_dtype, bias, bias_dtype, out, out_dtype, s); break;
+        default: launch_generic_m<8, true>(d, x, x_dtype, bias, bias_dtype, out, out_dtype, s); break;
+    }
+    return launch_check(err, errn, "raw twin generic gemv launch");
 }

@@ -66,8 +66,8 @@ def _dtype_code(dtype, what):
 
 
 def _is_twin(p: dict) -> bool:
-    """A twin dict: the raw bf16 weight, run by the raw kernel
-    (radix_ops.py:252-255)."""
+    """A twin dict: the raw bf16 weight, run by the compressed tensor's own
+    kernel with the decode replaced by a raw load (radix_ops.py:252-255)."""
     return p.get("codec") == "twin"
 
 
@@ -104,12 +104,38 @@ def _raw_rows(w: torch.Tensor, x: torch.Tensor, bias, out_dtype, what: str) -> t
     return out
 
 
+def _twin_rows(p: dict, x: torch.Tensor, bias, out_dtype) -> torch.Tensor:
+    """A twin dict's GEMV (dmx_radix_gemv_twin): the kernel its compressed
+    tensor runs (the dict's widths and block size), reading the raw weight in
+    place of the decode (radix_kernel_gpu.py:639-668), so its sums are the
+    compressed tensor's bit for bit."""
+    w = p["weight"]
+    if w.dim() != 2 or w.dtype != torch.bfloat16:
+        raise TypeError(f"raw gemv: the weight must be a 2-D bf16 tensor, got {w.dtype} {tuple(w.shape)}")
+    R, C = int(w.shape[0]), int(w.shape[1])
+    M = _check_rows(x, C, w.device, bias, R, "raw gemv")
+    w, x = w.contiguous(), x.contiguous()
+    out = torch.empty((M, R), dtype=out_dtype, device=x.device)
+    xd = _dtype_code(x.dtype, "activation")
+    od = _dtype_code(out_dtype, "output")
+    bias = bias.contiguous() if bias is not None else None
+    bd = _dtype_code(bias.dtype, "bias") if bias is not None else 0
+    widths = [int(v) for v in p.get("widths", (3, 8))]
+    warr = (ct.c_uint32 * len(widths))(*widths)
+    err = _native.error_buffer()
+    st = _native.lib().dmx_radix_gemv_twin(w.data_ptr(), R, C, int(p.get("block_size", 1024)), len(widths), warr,
+                                           x.data_ptr(), xd, M, bias.data_ptr() if bias is not None else None, bd,
+                                           out.data_ptr(), od, _stream(), err, len(err))
+    _native.check(st, err, "dmx_radix_gemv_twin")
+    return out
+
+
 def gemv_rows(p: dict, x: torch.Tensor, bias=None, out_dtype=torch.float32) -> torch.Tensor:
     """x [M, C] (bf16 or fp32, 1 <= M <= 8) -> [M, R] in out_dtype: the rows
     accumulated in fp32, the bias (bf16 or fp32, or None) added in fp32,
     one rounding."""
     if _is_twin(p):
-        return _raw_rows(p["weight"], x, bias, out_dtype, "raw gemv")
+        return _twin_rows(p, x, bias, out_dtype)
     R = int(p["R"])
     M = _check_rows(x, int(p["C"]), p["rx_data"].device, bias, R, "radix gemv")
     x = x.contiguous()

@@ -140,9 +140,7 @@ int dmx_radix_gemv_group(const dmx_radix_tensor* const* tensors, uint32_t n, con
 
 /* Replaces radix_ops.gemv_narrow (src/drinkme/codec/radix_ops.py:401-415),
  * the _gemv_narrow kernel (radix_ops.py:177-249) that swap.NarrowLinear
- * runs (src/drinkme/codec/swap.py:530-610), and the raw (twin) GEMV of
- * gemv_fused over a bf16 weight (radix_ops.py:252-255, stock_linear
- * swap.py:681-707): a raw bf16 weight, no codec.
+ * runs (src/drinkme/codec/swap.py:530-610): a raw bf16 weight, no codec.
  *   w     device [rows, cols] bf16 bits, row-major;
  *   x     device [m, cols], x_dtype DMX_BF16 or DMX_F32, row stride cols;
  *   m     1..8;
@@ -153,6 +151,25 @@ int dmx_radix_gemv_group(const dmx_radix_tensor* const* tensors, uint32_t n, con
  * bf16 x gives the same sums as its fp32 copy. */
 int dmx_gemv_narrow(const uint16_t* w, uint32_t rows, uint32_t cols, const void* x, int x_dtype, uint32_t m,
                     const void* bias, int bias_dtype, void* out, int out_dtype, void* stream, char* err, size_t errn);
+
+/* Replaces the raw twin of the GEMV calls: gemv_fused / gemv / gemv_mc over
+ * a twin dict (src/drinkme/codec/radix_ops.py:252-255; swap.to_device_twin
+ * swap.py:169-198, stock_linear swap.py:681-707), drinkme's kernels with
+ * RAW=True (the decode replaced by a load of the raw weight,
+ * radix_kernel_gpu.py:639-668). The kernel is the one dmx_radix_gemv runs
+ * for a radix tensor of this shape, block size and widths (the twin dict's
+ * widths are its compressed tensor's profile; sip's (3, 8) for a plain
+ * Linear), with the weight read at each block's (row, column) in place of
+ * the decode: the same work split and the same sums in the same order, so
+ * the output equals dmx_radix_gemv's on the packed tensor bit for bit when
+ * w is the packed tensor's source. w is 16-byte aligned for the fast
+ * kernels (else the generic kernel's order applies).
+ *   w        device [rows, cols] bf16 bits, row-major;
+ *   widths   n_widths tier widths (2..8, the last 8), as the radix tensor's;
+ *   x, m, bias, out as dmx_radix_gemv. */
+int dmx_radix_gemv_twin(const uint16_t* w, uint32_t rows, uint32_t cols, uint32_t block_size, uint32_t n_widths,
+                        const uint32_t* widths, const void* x, int x_dtype, uint32_t m, const void* bias,
+                        int bias_dtype, void* out, int out_dtype, void* stream, char* err, size_t errn);
 
 /* One tensor file of a drinkme pack (.npz: stored .npy members and a
  * `scalars` JSON blob; src/drinkme/codec/pack.py:509-520, :629-644). */
