@@ -34,14 +34,18 @@ def _check_bound(y, x_f32, bits, what):
     return ref
 
 
-def _run_shape(cuda, bits, profile, rng, ms=(1, 3, 8)):
+def _run_shape(cuda, bits, profile, rng, ms=(1, 3, 8), stored_raw=False):
     import torch
 
     from drinkme_amd import radix_ops, swap
 
     R, C = bits.shape
-    d = oracle_dict(bits, profile)
-    rt = swap.to_device_radix(d, cuda)
+    if stored_raw:
+        # the tensor drinkme stores raw (radix would expand it): served from
+        # its raw bits, here through the twin of the profile's widths
+        rt = swap.to_device_twin(bf16_tensor(bits, cuda), widths=O.PROFILES[profile], device=cuda)
+    else:
+        rt = swap.to_device_radix(oracle_dict(bits, profile), cuda)
     bias_bits = O.f32_to_bf16_bits(np.linspace(-0.1, 0.1, R).astype(np.float32))
     bias = bf16_tensor(bias_bits, cuda)
     for M in ms:
@@ -71,10 +75,9 @@ def _run_shape(cuda, bits, profile, rng, ms=(1, 3, 8)):
 def test_ragged_shapes(cuda, shape, spread, profile):
     rng = np.random.default_rng(zlib.crc32(repr((shape, spread, profile)).encode()))
     bits = finite_bits(rng, shape, spread)
-    if O.pack(bits, profile).raw:
-        pytest.skip("radix would expand this tensor (stored raw)")
-    print(f"case gemv ragged {shape} spread={spread} {profile}", flush=True)
-    _run_shape(cuda, bits, profile, rng)
+    raw = O.pack(bits, profile).raw  # (1, 1): radix would expand it, so it is stored raw
+    print(f"case gemv ragged {shape} spread={spread} {profile} raw={raw}", flush=True)
+    _run_shape(cuda, bits, profile, rng, stored_raw=raw)
 
 
 @pytest.mark.parametrize("shape", [(1024, 4096), (256, 12288), (4096, 1024)])
