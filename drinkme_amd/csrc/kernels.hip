@@ -619,7 +619,7 @@ struct SipCursor {
 // among the workgroup's two, its column phase, and whether it closes its
 // unit.
 struct SipRef {
-    uint32_t slot, cb, t, p;
+    uint32_t slot, cb, t, p;  // (decode mode: t is the block's index in its tensor, the output's block)
     bool last;
 };
 
@@ -780,10 +780,18 @@ __device__ __forceinline__ void sip_table(uint2* tb, const uint32_t* palette) {
 // PH: the activation columns come in phases (sh.phases > 1), for rows too
 // long for LDS; the other instantiations carry no phase code. (With M = 4
 // too, it keeps one workgroup per CU, for the registers.)
-template <bool TWO, int M, bool PH, int RAW = 0>
+// MODE: 0 the GEMV; 1, 2 the raw twin (the decode replaced by a load of the
+// raw weight) mirroring the sip or the gulp kernel's matrix-core rule; 3
+// decode only: each block's bf16 bits stored to the tensor's output
+// (row-major [rows, cols]) in place of the products.
+constexpr int kModeGemv = 0, kModeTwinSip = 1, kModeTwinGulp = 2, kModeDecode = 3;
+
+template <bool TWO, int M, bool PH, int MODE = kModeGemv>
 __global__ __launch_bounds__(kSipThreads, (M == 8 || (PH && M == 4)) ? 3 : 6) void k_gemv_sip(const SipGroup g, const uint16_t* __restrict__ x,
                                                           const SipShape sh) {
-    static_assert(!(TWO && RAW), "the raw twin runs one tensor");
+    constexpr bool RAW = MODE == kModeTwinSip || MODE == kModeTwinGulp, DEC = MODE == kModeDecode;
+    static_assert(!(TWO && MODE), "the raw twin and the decode run one tensor");
+    static_assert(!DEC || (M == 1 && !PH), "the decode runs unphased");
     // fixed-size tables in static LDS (their addresses fold into the LDS
     // instructions' offsets); the activation, the row partials and a second
     // tensor's table after them
@@ -827,7 +835,7 @@ __global__ __launch_bounds__(kSipThreads, (M == 8 || (PH && M == 4)) ? 3 : 6) vo
     // the activation (its first column phase) goes to LDS by direct loads
     // (no registers staged), first in the queue: small and hot in L2; the
     // barrier below waits for it
-    load_x_slice<M, kSipThreads>(sh, x, xs, 0);
+    if constexpr (!DEC) load_x_slice<M, kSipThreads>(sh, x, xs, 0);
 
     // the first two blocks' loads go out before the tables are built; a
     // cursor past the wave's work reads the workgroup's first block instead
@@ -851,7 +859,7 @@ __global__ __launch_bounds__(kSipThreads, (M == 8 || (PH && M == 4)) ? 3 : 6) vo
     SipRef nr;  // the last next_offsets() block
     auto next_offsets = [&]() {
         const bool live = p.p < sh.phases;
-        nr.t = TWO && live ? p.t : 0u;
+        nr.t = DEC ? p.blk : TWO && live ? p.t : 0u;
         nr.slot = p.slot;
         nr.cb = p.cb;
         nr.p = p.p;
@@ -860,7 +868,7 @@ __global__ __launch_bounds__(kSipThreads, (M == 8 || (PH && M == 4)) ? 3 : 6) vo
         if constexpr (RAW)  // the block's byte offset from the workgroup's first row
             o = make_uint2(((live ? p.blk : sp.a_first) - sp.a_first) * 2048u, 0u);
         else
-            o = sip_offsets(nr.t ? offsets_b : offsets_a, live ? p.blk : sp.a_first);
+            o = sip_offsets(TWO && nr.t ? offsets_b : offsets_a, live ? p.blk : sp.a_first);
         sip_next<TWO>(sh, p, wk, sp);
         return o;
     };
@@ -913,7 +921,7 @@ __global__ __launch_bounds__(kSipThreads, (M == 8 || (PH && M == 4)) ? 3 : 6) vo
     // M = 1 keeps two accumulator chains; M > 1 one per row
     float acc0 = 0.0f, acc1 = 0.0f;
     // verify rows on the matrix cores (a raw twin mirroring gulp: gulp's rule)
-    constexpr bool MF = RAW == 2 ? gulp_mfma(M) : sip_mfma(M);
+    constexpr bool MF = MODE == kModeTwinGulp ? gulp_mfma(M) : sip_mfma(M);
     constexpr int MA = MF ? 1 : M, MD = MF ? M : 1;
     float acc[MA];
 #pragma unroll
@@ -1042,6 +1050,13 @@ __global__ __launch_bounds__(kSipThreads, (M == 8 || (PH && M == 4)) ? 3 : 6) vo
         wp[6] = (__builtin_amdgcn_perm(L3, L3, 0x01010000) & keep) | (E3.x & ~keep);
         wp[7] = (__builtin_amdgcn_perm(L3, L3, 0x03030202) & keep) | (E3.y & ~keep);
         }
+        if constexpr (DEC) {
+            // the lane's 16 weights: 32 bytes at weight 1024 blk + 16 lane
+            uint4* d = reinterpret_cast<uint4*>(pick(g.out, ia)) + (uint64_t)c.t * 128u + 2u * lane;
+            d[0] = make_uint4(wp[0], wp[1], wp[2], wp[3]);
+            d[1] = make_uint4(wp[4], wp[5], wp[6], wp[7]);
+            return;
+        }
         if (M == 1) {
             acc0 = dot2(wp[0], xa.x, acc0);
             acc1 = dot2(wp[1], xa.y, acc1);
@@ -1120,6 +1135,7 @@ __global__ __launch_bounds__(kSipThreads, (M == 8 || (PH && M == 4)) ? 3 : 6) vo
     if (k < items) process(sA, rA);
     if constexpr (RAW) RAW_WAIT(0, sB); else SIP_WAIT(0, sB);
     if (k + 1 < items) process(sB, rB);
+    if constexpr (DEC) return;  // every load has landed (the waits above)
     if (PH)
         while (cur_phase + 1 < sh.phases) phase_advance();
     __syncthreads();
@@ -1177,6 +1193,9 @@ __global__ __launch_bounds__(kSipThreads, (M == 8 || (PH && M == 4)) ? 3 : 6) vo
 constexpr uint32_t kGulpFixed = 256 + 64;  // literal plane + tier 0 words of a 1024-weight block
 constexpr uint32_t kGulpT0Bytes = 256 * 8;
 constexpr uint32_t kGulpX2Words = 40;     // per wave: 128 exponent bytes + a window's overhang
+// static LDS of the sip and gulp kernels (their tables), for the host's plans
+constexpr size_t kSipStaticLds = kTableBytes + kSelBytes;
+constexpr size_t kGulpStaticLds = kGulpT0Bytes + kTableBytes + 13 * 16 * 8 + 16 + kSipWaves * kGulpX2Words * 4;
 
 struct GulpStage {
     u32x4 lit;
@@ -1271,9 +1290,12 @@ __device__ __forceinline__ void gulp_tables(uint2* t0tab, uint2* t1tab, uint8_t*
     if (t < 4) reinterpret_cast<uint32_t*>(pal2)[t] = t == 0 ? p2 : t == 1 ? p3 : t == 2 ? p4 : p5;
 }
 
-template <int M, bool PH>
+// DEC: decode only, each block's bf16 bits stored to the tensor's output
+// (row-major [rows, cols]) in place of the products.
+template <int M, bool PH, bool DEC = false>
 __global__ __launch_bounds__(kSipThreads, (M == 8 || (PH && M == 4)) ? 3 : 6) void k_gemv_gulp(const SipGroup g, const uint16_t* __restrict__ x,
                                                                         const SipShape sh) {
+    static_assert(!DEC || (M == 1 && !PH), "the decode runs unphased");
     constexpr int W = kSipWaves, TH = kSipThreads;
     __shared__ uint2 t0tab[256];
     __shared__ uint2 t1tab[4096];
@@ -1311,7 +1333,7 @@ __global__ __launch_bounds__(kSipThreads, (M == 8 || (PH && M == 4)) ? 3 : 6) vo
     uint32_t* x2 = x2_all + wv * kGulpX2Words;
 
     // the activation rows (first column phase), as in the sip kernel
-    load_x_slice<M, TH>(sh, x, xs, 0);
+    if constexpr (!DEC) load_x_slice<M, TH>(sh, x, xs, 0);
 
     SipCursor p, c;
     const SipWalk wk = sip_walk(sh, nrows);
@@ -1536,6 +1558,14 @@ __global__ __launch_bounds__(kSipThreads, (M == 8 || (PH && M == 4)) ? 3 : 6) vo
         wp[5] = (__builtin_amdgcn_perm(L2, L2, 0x03030202) & keep) | (E2.y & ~keep);
         wp[6] = (__builtin_amdgcn_perm(L3, L3, 0x01010000) & keep) | (E3.x & ~keep);
         wp[7] = (__builtin_amdgcn_perm(L3, L3, 0x03030202) & keep) | (E3.y & ~keep);
+        if constexpr (DEC) {
+            // the lane's 16 weights: 32 bytes at weight 1024 blk + 16 lane
+            uint4* d = reinterpret_cast<uint4*>(pick(g.out, ia)) + (uint64_t)c.blk * 128u + 2u * lane;
+            d[0] = make_uint4(wp[0], wp[1], wp[2], wp[3]);
+            d[1] = make_uint4(wp[4], wp[5], wp[6], wp[7]);
+            sip_next<false>(sh, c, wk, sp);
+            return;
+        }
         if (M == 1) {
             acc0 = dot2(wp[0], xa.x, acc0);
             acc1 = dot2(wp[1], xa.y, acc1);
@@ -1621,6 +1651,7 @@ __global__ __launch_bounds__(kSipThreads, (M == 8 || (PH && M == 4)) ? 3 : 6) vo
     if (k < items) process(sA);
     GULP_WAIT(0, sB);
     if (k + 1 < items) process(sB);
+    if constexpr (DEC) return;  // every load has landed (the waits above)
     if (PH)
         while (cur_phase + 1 < sh.phases) phase_advance();
     __syncthreads();
@@ -1954,7 +1985,7 @@ int launch_sip(const dmx_radix_tensor* const* ts, uint32_t n, const void* x, uin
     sh.m = m;
     sh.bias_dtype = bias_dtype;
     sh.out_dtype = out_dtype;
-    const size_t fixed = kTableBytes + kSelBytes;
+    const size_t fixed = kSipStaticLds;
     uint32_t grid = 0;
     size_t lds = 0;
     bool two = false;
@@ -2029,7 +2060,7 @@ int launch_gulp(const dmx_radix_tensor* const* ts, uint32_t n, const void* x, ui
     sh.tbl2_lds = 0;
     sh.bias_dtype = bias_dtype;
     sh.out_dtype = out_dtype;
-    const size_t fixed = kGulpT0Bytes + kTableBytes + 13 * 16 * 8 + 16 + kSipWaves * kGulpX2Words * 4;
+    const size_t fixed = kGulpStaticLds;
     uint32_t grid = 0;
     size_t lds = 0;
     bool two = false;
@@ -2114,10 +2145,64 @@ extern "C" int dmx_radix_set_policy(int policy) {
     return g_policy.exchange(policy);
 }
 
+// The decode of a whole-block sip or gulp tensor on its fast kernel's work
+// split and decode (decode mode: the bits stored in place of the products).
+// Returns 2, having launched nothing, when the tensor is not one of those
+// (or would need column phases); the generic decoder then runs.
+int launch_decode_fast(const dmx_radix_tensor* t, uint16_t* out, hipStream_t stream, char* err, size_t errn) {
+    const bool sip = is_sip(t);
+    const bool gulp = is_gulp(t) && t->schedule && (reinterpret_cast<uintptr_t>(t->schedule) & 3u) == 0;
+    if (g_policy.load() != DMX_POLICY_AUTO || !(sip || gulp) || t->block_size != 1024 || t->cols % 1024 != 0 ||
+        (reinterpret_cast<uintptr_t>(out) & 15u) != 0)
+        return 2;
+    SipGroup g;
+    SipShape sh;
+    for (uint32_t i = 0; i < (uint32_t)kGroupMax; ++i) {
+        g.data[i] = t->data;
+        g.offsets[i] = t->offsets;
+        g.palette[i] = t->palette;
+        g.schedule[i] = t->schedule;
+        g.bias[i] = nullptr;
+        g.out[i] = out;
+        g.row0[i] = i == 0 ? 0u : t->rows;
+    }
+    g.row0[kGroupMax] = t->rows;
+    sh.rows = t->rows;
+    sh.cols = t->cols;
+    sh.nb = t->cols / 1024;
+    sh.n = 1;
+    sh.m = 1;
+    sh.tbl2_lds = 0;
+    sh.bias_dtype = sh.out_dtype = 0;
+    const size_t fixed = sip ? kSipStaticLds : kGulpStaticLds;
+    uint32_t grid = 0;
+    size_t lds = 0;
+    bool two = false;
+    if (!plan_launch(sh, g, 1, t->rows, 1, kSipWaves, false, fixed, sip, grid, lds, two) || sh.phases > 1) return 2;
+    const void* kern = sip ? reinterpret_cast<const void*>(k_gemv_sip<false, 1, false, kModeDecode>)
+                           : reinterpret_cast<const void*>(k_gemv_gulp<1, false, true>);
+    static std::atomic<size_t> sip_opted{64 * 1024 - kSipStaticLds}, gulp_opted{64 * 1024 - kGulpStaticLds};
+    std::atomic<size_t>& opted = sip ? sip_opted : gulp_opted;
+    if (lds > opted.load()) {
+        hipError_t e = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return fail_hip(err, errn, "decode kernel LDS opt-in", e);
+        opted.store(lds);
+    }
+    if (sip)
+        hipLaunchKernelGGL((k_gemv_sip<false, 1, false, kModeDecode>), dim3(grid), dim3(kSipThreads), lds, stream, g,
+                           static_cast<const uint16_t*>(nullptr), sh);
+    else
+        hipLaunchKernelGGL((k_gemv_gulp<1, false, true>), dim3(grid), dim3(kSipThreads), lds, stream, g,
+                           static_cast<const uint16_t*>(nullptr), sh);
+    return launch_check(err, errn, "decode launch");
+}
+
 extern "C" int dmx_radix_decode(const dmx_radix_tensor* t, uint16_t* out, void* stream, char* err, size_t errn) {
     Desc d;
     if (check_tensor(t, d, err, errn)) return 1;
     if (!out) return fail(err, errn, "null output");
+    const int rc = launch_decode_fast(t, out, static_cast<hipStream_t>(stream), err, errn);
+    if (rc != 2) return rc;
     hipLaunchKernelGGL(k_decode, dim3(d.rows * d.nb), dim3(kGenThreads), 0, static_cast<hipStream_t>(stream), d, out);
     return launch_check(err, errn, "decode launch");
 }
@@ -2250,8 +2335,7 @@ int launch_raw(const uint16_t* w, uint32_t rows, uint32_t cols, bool gulp, const
     sh.tbl2_lds = 0;
     sh.bias_dtype = bias_dtype;
     sh.out_dtype = out_dtype;
-    const size_t sip_fixed = kTableBytes + kSelBytes;
-    const size_t fixed = gulp ? kGulpT0Bytes + kTableBytes + 13 * 16 * 8 + 16 + kSipWaves * kGulpX2Words * 4 : sip_fixed;
+    const size_t fixed = gulp ? kGulpStaticLds : kSipStaticLds;
     uint32_t grid = 0;
     size_t lds = 0;
     bool two = false;
@@ -2259,7 +2343,7 @@ int launch_raw(const uint16_t* w, uint32_t rows, uint32_t cols, bool gulp, const
                      lds, two))
         return 2;
     if ((uint64_t)sh.rows_per_wg * cols * 2 >= (1ull << 31)) return 2;  // a tile's bytes within the buffer range
-    static std::atomic<size_t> lds_opted{64 * 1024 - sip_fixed};  // the raw kernels declare sip's static LDS
+    static std::atomic<size_t> lds_opted{64 * 1024 - kSipStaticLds};  // the raw kernels declare sip's static LDS
     if (lds > lds_opted.load()) {
         for (int t = 0; t < 2; ++t)
             for (int i = 0; i < 5; ++i) {

@@ -12,7 +12,7 @@ import numpy as np
 import pytest
 
 from oracle import radix_oracle as O
-from tests.helpers import all_patterns, finite_bits, oracle_dict, u16_of
+from tests.helpers import all_patterns, escape_heavy_bits, finite_bits, oracle_dict, u16_of
 
 pytestmark = pytest.mark.gpu
 
@@ -54,3 +54,31 @@ def test_ragged_and_production_shapes_decode_exactly(cuda, shape, spread):
         assert np.array_equal(u16_of(radix_ops.decode_bits(rt)), bits)
         if len(d["widths"]) > 2:
             assert np.array_equal(u16_of(rt["rx_schedule"]), O.schedule(p))
+
+
+@pytest.mark.parametrize("profile", ["sip", "gulp"])
+def test_fast_decode_of_whole_block_tensors(cuda, profile):
+    """Whole-block sip and gulp tensors decode on their GEMV kernel's work
+    split (decode mode): every bf16 pattern laid out in whole blocks, and
+    escape-heavy tensors (the terminal path, and for sip a terminal longer
+    than 64 words), each equal to the source and to the generic decoder."""
+    from drinkme_amd import radix_ops, swap
+
+    rng = np.random.default_rng(5 + len(profile))
+    cases = {"all patterns": all_patterns((64, 2048)),
+             "escapes 3%": escape_heavy_bits(rng, (300, 4096), 0.03),
+             "escapes 45%": escape_heavy_bits(rng, (64, 4096), 0.45),
+             "tall": finite_bits(rng, (2050, 2048), spread=True)}
+    for name, bits in cases.items():
+        if O.pack(bits, profile).raw:
+            continue
+        print(f"case fast decode {profile} {name}", flush=True)
+        rt = swap.to_device_radix(oracle_dict(bits, profile), cuda)
+        fast = u16_of(radix_ops.decode_bits(rt))
+        assert np.array_equal(fast, bits), f"{profile} {name}"
+        prev = radix_ops.set_policy("generic")
+        try:
+            generic = u16_of(radix_ops.decode_bits(rt))
+        finally:
+            radix_ops.set_policy(prev)
+        assert np.array_equal(generic, fast)
