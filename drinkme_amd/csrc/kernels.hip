@@ -559,7 +559,9 @@ __device__ __forceinline__ i32x4 make_rsrc(const void* base, uint32_t bytes) {
 }
 
 // A block's loads through its tensor's buffer resource (based at the
-// workgroup's first block of that tensor, so every byte offset is small):
+// workgroup's first block of that tensor, so every byte offset is small),
+// non-temporal (`nt`): a sweep reads each weight once, and keeping the
+// stream out of the caches measured 2.7% faster on the Qwen3-8B step:
 // the terminal word, the tier-0 pair and the literals, issued as one unit of
 // three vector loads. They are written as instructions the compiler does
 // not track, so the only waits on them are the explicit SIP_WAIT below,
@@ -574,9 +576,9 @@ __device__ __forceinline__ SipStage sip_load(i32x4 rsrc, uint32_t base, uint2 o,
     s.t = t;
     const uint32_t soff = (o.x - base) * 4u;
     asm volatile(
-        "buffer_load_dword %0, %3, %6, %7 offen\n\t"
-        "buffer_load_dwordx2 %1, %4, %6, %7 offen\n\t"
-        "buffer_load_dwordx4 %2, %5, %6, %7 offen"
+        "buffer_load_dword %0, %3, %6, %7 offen nt\n\t"
+        "buffer_load_dwordx2 %1, %4, %6, %7 offen nt\n\t"
+        "buffer_load_dwordx4 %2, %5, %6, %7 offen nt"
         : "=&v"(s.term), "=&v"(s.t0), "=&v"(s.lit)
         : "v"(ln.term), "v"(ln.t0), "v"(ln.lit), "s"(rsrc), "s"(soff));
     return s;
@@ -595,8 +597,8 @@ __device__ __forceinline__ SipStage raw_load(i32x4 rsrc, uint32_t off, const Sip
     SipStage s;
     s.start = s.end = s.t = 0;
     asm volatile(
-        "buffer_load_dwordx4 %0, %2, %3, %4 offen\n\t"
-        "buffer_load_dwordx4 %1, %2, %3, %4 offen offset:16"
+        "buffer_load_dwordx4 %0, %2, %3, %4 offen nt\n\t"
+        "buffer_load_dwordx4 %1, %2, %3, %4 offen offset:16 nt"
         : "=&v"(s.lit), "=&v"(s.hi)
         : "v"(ln.raw), "s"(rsrc), "s"(off));
     return s;
@@ -1227,11 +1229,11 @@ __device__ __forceinline__ GulpStage gulp_load(i32x4 rsrc, uint32_t base, uint2 
     const uint32_t soff2 = soff + 4u * (kGulpFixed + w1);
     const uint32_t soff3 = soff2 + 4u * w2;
     asm volatile(
-        "buffer_load_dword %0, %5, %8, %10 offen\n\t"
-        "buffer_load_dword %1, %6, %8, %9 offen\n\t"
-        "buffer_load_dword %2, %5, %8, %11 offen offset:1280\n\t"
-        "buffer_load_dword %3, %5, %8, %11 offen offset:1024\n\t"
-        "buffer_load_dwordx4 %4, %7, %8, %11 offen"
+        "buffer_load_dword %0, %5, %8, %10 offen nt\n\t"
+        "buffer_load_dword %1, %6, %8, %9 offen nt\n\t"
+        "buffer_load_dword %2, %5, %8, %11 offen offset:1280 nt\n\t"
+        "buffer_load_dword %3, %5, %8, %11 offen offset:1024 nt\n\t"
+        "buffer_load_dwordx4 %4, %7, %8, %11 offen nt"
         : "=&v"(s.term), "=&v"(s.t2), "=&v"(s.t1), "=&v"(s.t0), "=&v"(s.lit)
         : "v"(ln.w), "v"(ln.t2), "v"(ln.lit), "s"(rsrc), "s"(soff2), "s"(soff3), "s"(soff));
     return s;
