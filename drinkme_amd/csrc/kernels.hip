@@ -31,6 +31,8 @@
 
 #include <algorithm>
 #include <atomic>
+#include <map>
+#include <mutex>
 #include <cmath>
 #include <numeric>
 
@@ -1773,6 +1775,28 @@ int fail_hip(char* err, size_t n, const char* what, hipError_t e) {
     return fail(err, n, buf);
 }
 
+// Raises the dynamic-LDS limit of a kernel family (its nk kernels) on the
+// current device to at least `lds`. The limit only ever goes up, under one
+// lock, so a concurrent caller cannot lower a limit another call's launch
+// relies on. `preset` is the limit a kernel has before any opt-in.
+enum LdsFamily { kFamSip, kFamGulp, kFamRaw, kFamDecodeSip, kFamDecodeGulp };
+int raise_lds_limit(LdsFamily family, const void* const* kerns, int nk, size_t lds, size_t preset, const char* what,
+                    char* err, size_t errn) {
+    static std::mutex mu;
+    static std::map<std::pair<int, int>, size_t> limit;  // (family, device) -> dynamic LDS allowed
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess) dev = -1;
+    std::lock_guard<std::mutex> lock(mu);
+    size_t& cur = limit.try_emplace(std::make_pair((int)family, dev), preset).first->second;
+    if (lds <= cur) return 0;
+    for (int i = 0; i < nk; ++i) {
+        const hipError_t e = hipFuncSetAttribute(kerns[i], hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return fail_hip(err, errn, what, e);
+    }
+    cur = lds;
+    return 0;
+}
+
 std::atomic<int> g_policy{DMX_POLICY_AUTO};
 
 uint64_t pad_words_for(uint32_t block, const uint32_t* w, uint32_t nw) {
@@ -1992,15 +2016,11 @@ int launch_sip(const dmx_radix_tensor* const* ts, uint32_t n, const void* x, uin
     size_t lds = 0;
     bool two = false;
     if (!plan_launch(sh, g, n, min_rows, M, kSipWaves, sip_mfma((int)M), fixed, true, grid, lds, two)) return 2;
-    static std::atomic<size_t> lds_opted{64 * 1024 - fixed};
-    if (lds > lds_opted.load()) {
+    {
+        const void* kerns[12];
         for (int t = 0; t < 3; ++t)
-            for (int i = 0; i < 4; ++i) {
-                hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(sip_kernel(t, i)),
-                                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-                if (e != hipSuccess) return fail_hip(err, errn, "sip kernel LDS opt-in", e);
-            }
-        lds_opted.store(lds);
+            for (int i = 0; i < 4; ++i) kerns[4 * t + i] = reinterpret_cast<const void*>(sip_kernel(t, i));
+        if (raise_lds_limit(kFamSip, kerns, 12, lds, 64 * 1024 - fixed, "sip kernel LDS opt-in", err, errn)) return 1;
     }
     hipLaunchKernelGGL(sip_kernel(sh.phases > 1 ? 2 : two ? 1 : 0, mi), dim3(grid), dim3(kSipThreads), lds, stream, g,
                        static_cast<const uint16_t*>(x), sh);
@@ -2067,15 +2087,11 @@ int launch_gulp(const dmx_radix_tensor* const* ts, uint32_t n, const void* x, ui
     size_t lds = 0;
     bool two = false;
     if (!plan_launch(sh, g, n, min_rows, M, kSipWaves, gulp_mfma((int)M), fixed, false, grid, lds, two)) return 2;
-    static std::atomic<size_t> lds_opted{64 * 1024 - fixed};
-    if (lds > lds_opted.load()) {
+    {
+        const void* kerns[8];
         for (int t = 0; t < 2; ++t)
-            for (int i = 0; i < 4; ++i) {
-                hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(gulp_kernel(t, i)),
-                                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-                if (e != hipSuccess) return fail_hip(err, errn, "gulp kernel LDS opt-in", e);
-            }
-        lds_opted.store(lds);
+            for (int i = 0; i < 4; ++i) kerns[4 * t + i] = reinterpret_cast<const void*>(gulp_kernel(t, i));
+        if (raise_lds_limit(kFamGulp, kerns, 8, lds, 64 * 1024 - fixed, "gulp kernel LDS opt-in", err, errn)) return 1;
     }
     hipLaunchKernelGGL(gulp_kernel(sh.phases > 1, mi), dim3(grid), dim3(kSipThreads), lds, stream, g,
                        static_cast<const uint16_t*>(x), sh);
@@ -2183,13 +2199,9 @@ int launch_decode_fast(const dmx_radix_tensor* t, uint16_t* out, hipStream_t str
     if (!plan_launch(sh, g, 1, t->rows, 1, kSipWaves, false, fixed, sip, grid, lds, two) || sh.phases > 1) return 2;
     const void* kern = sip ? reinterpret_cast<const void*>(k_gemv_sip<false, 1, false, kModeDecode>)
                            : reinterpret_cast<const void*>(k_gemv_gulp<1, false, true>);
-    static std::atomic<size_t> sip_opted{64 * 1024 - kSipStaticLds}, gulp_opted{64 * 1024 - kGulpStaticLds};
-    std::atomic<size_t>& opted = sip ? sip_opted : gulp_opted;
-    if (lds > opted.load()) {
-        hipError_t e = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        if (e != hipSuccess) return fail_hip(err, errn, "decode kernel LDS opt-in", e);
-        opted.store(lds);
-    }
+    if (raise_lds_limit(sip ? kFamDecodeSip : kFamDecodeGulp, &kern, 1, lds, 64 * 1024 - fixed,
+                        "decode kernel LDS opt-in", err, errn))
+        return 1;
     if (sip)
         hipLaunchKernelGGL((k_gemv_sip<false, 1, false, kModeDecode>), dim3(grid), dim3(kSipThreads), lds, stream, g,
                            static_cast<const uint16_t*>(nullptr), sh);
@@ -2345,15 +2357,13 @@ int launch_raw(const uint16_t* w, uint32_t rows, uint32_t cols, bool gulp, const
                      lds, two))
         return 2;
     if ((uint64_t)sh.rows_per_wg * cols * 2 >= (1ull << 31)) return 2;  // a tile's bytes within the buffer range
-    static std::atomic<size_t> lds_opted{64 * 1024 - kSipStaticLds};  // the raw kernels declare sip's static LDS
-    if (lds > lds_opted.load()) {
+    {
+        const void* kerns[10];  // (the raw kernels declare sip's static LDS)
         for (int t = 0; t < 2; ++t)
-            for (int i = 0; i < 5; ++i) {
-                hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(raw_kernel(t, i & 3, i == 4)),
-                                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-                if (e != hipSuccess) return fail_hip(err, errn, "raw twin kernel LDS opt-in", e);
-            }
-        lds_opted.store(lds);
+            for (int i = 0; i < 5; ++i) kerns[5 * t + i] = reinterpret_cast<const void*>(raw_kernel(t, i & 3, i == 4));
+        if (raise_lds_limit(kFamRaw, kerns, 10, lds, 64 * 1024 - kSipStaticLds, "raw twin kernel LDS opt-in", err,
+                            errn))
+            return 1;
     }
     hipLaunchKernelGGL(raw_kernel(sh.phases > 1, mi, gulp), dim3(grid), dim3(kSipThreads), lds, stream, g,
                        static_cast<const uint16_t*>(x), sh);

@@ -245,3 +245,50 @@ def test_gulp_fast_path(cuda, kind, M):
     finally:
         radix_ops.set_policy(prev)
     _check_bound(yg, O.bf16_bits_to_f32(xb), bits, f"gulp {kind} M={M} generic")
+
+
+def test_threads_with_different_lds_needs(cuda):
+    """Launches from several host threads (a stream each) whose plans need
+    different dynamic-LDS limits: every call succeeds and equals the
+    single-threaded result bit for bit (the limit only ever rises)."""
+    import threading
+
+    import torch
+
+    from drinkme_amd import radix_ops, swap
+
+    rng = np.random.default_rng(31)
+    shapes = [(256, 2048), (128, 16384), (256, 32768)]
+    rts, xs, want = [], [], []
+    for R, C in shapes:
+        bits = finite_bits(rng, (R, C))
+        rt = swap.to_device_radix(oracle_dict(bits, "sip"), cuda)
+        x = bf16_tensor(O.f32_to_bf16_bits(rng.standard_normal((8, C)).astype(np.float32)), cuda)
+        rts.append(rt)
+        xs.append(x)
+    for rt, x in zip(rts, xs):
+        want.append([radix_ops.gemv_mc(rt, x[:m]) for m in (2, 4, 8)])
+    torch.cuda.synchronize()
+    errors = []
+
+    def worker(k):
+        try:
+            s = torch.cuda.Stream()
+            with torch.cuda.stream(s):
+                for it in range(6):
+                    i = (k + it) % len(shapes)
+                    for j, m in enumerate((2, 4, 8)):
+                        got = radix_ops.gemv_mc(rts[i], xs[i][:m])
+                        s.synchronize()
+                        if not torch.equal(got, want[i][j]):
+                            errors.append(f"thread {k} shape {shapes[i]} M={m}")
+        except Exception as e:  # noqa: BLE001 - reported below
+            errors.append(f"thread {k}: {e}")
+
+    print("case threads lds", flush=True)
+    ts = [threading.Thread(target=worker, args=(k,)) for k in range(4)]
+    for t in ts:
+        t.start()
+    for t in ts:
+        t.join()
+    assert not errors, errors
