@@ -341,8 +341,11 @@ constexpr int kSipThreads = kSipWaves * kWave;
 // behind the first (its activation loads queue behind the first's payload
 // misses) and only adds dispatch and setup: one per CU measured 2% faster
 // on the Qwen3-8B step and 12% on 4096 x 4096 GEMVs. gulp: two, as its
-// decode is bound by instruction latency and needs the waves.
-constexpr uint32_t kSipPerCu = 1, kGulpPerCu = 2;
+// decode is bound by instruction latency and needs the waves. The decode
+// mode (2 KB stored per block): two, measured 3-11% faster than one. A sip
+// launch of at least kSipTwoPerCuBlocks blocks per CU also takes two: at
+// 2374 per CU (Qwen3-8B's lm_head) one was 3% slower.
+constexpr uint32_t kSipPerCu = 1, kGulpPerCu = 2, kDecodePerCu = 2, kSipTwoPerCuBlocks = 1500;
 constexpr uint32_t kSipFixed = 256 + 96;  // literal plane + tier 0 words of a 1024-weight block
 constexpr uint32_t kTableBytes = 4096 * 8;
 constexpr uint32_t kSelBytes = (16 + 13 * 16) * 8;
@@ -1898,6 +1901,8 @@ bool plan_launch(SipShape& sh, const SipGroup& g, uint32_t n, uint32_t min_rows,
                  uint32_t max_per_cu, bool mf, size_t fixed, bool allow_two, uint32_t& grid_out, size_t& lds_out,
                  bool& two_out) {
     const uint32_t cus = (uint32_t)cu_count();
+    // (a launch of many blocks per CU, such as lm_head, keeps two)
+    if (max_per_cu == 1 && (uint64_t)sh.rows * sh.nb >= (uint64_t)kSipTwoPerCuBlocks * cus) max_per_cu = 2;
     for (uint32_t per_cu = M == 8 ? 1 : max_per_cu; per_cu >= 1; --per_cu) {
         uint32_t grid = std::min<uint32_t>(sh.rows, cus * per_cu);
         uint32_t T = (sh.rows + grid - 1) / grid;
@@ -2206,7 +2211,7 @@ int launch_decode_fast(const dmx_radix_tensor* t, uint16_t* out, hipStream_t str
     uint32_t grid = 0;
     size_t lds = 0;
     bool two = false;
-    if (!plan_launch(sh, g, 1, t->rows, 1, kSipWaves, sip ? kSipPerCu : kGulpPerCu, false, fixed, sip, grid, lds, two) ||
+    if (!plan_launch(sh, g, 1, t->rows, 1, kSipWaves, kDecodePerCu, false, fixed, sip, grid, lds, two) ||
         sh.phases > 1)
         return 2;
     const void* kern = sip ? reinterpret_cast<const void*>(k_gemv_sip<false, 1, false, kModeDecode>)
