@@ -346,6 +346,11 @@ constexpr int kSipThreads = kSipWaves * kWave;
 // launch of at least kSipTwoPerCuBlocks blocks per CU also takes two: at
 // 2374 per CU (Qwen3-8B's lm_head) one was 3% slower.
 constexpr uint32_t kSipPerCu = 1, kGulpPerCu = 2, kDecodePerCu = 2, kSipTwoPerCuBlocks = 1500;
+// The sip kernel's progress balance (below): a margin of 12 measured best
+// of 0, 6, 12, 24 and 48; on for launches of 12 or more blocks a wave (the
+// Qwen3-8B step 1.9% faster than without, one layer 2.6%, 4096 x 4096
+// GEMVs unchanged, which were 4-6% slower with it on).
+constexpr uint32_t kBalanceMargin = 12, kBalanceMinBlocks = 12;
 constexpr uint32_t kSipFixed = 256 + 96;  // literal plane + tier 0 words of a 1024-weight block
 constexpr uint32_t kTableBytes = 4096 * 8;
 constexpr uint32_t kSelBytes = (16 + 13 * 16) * 8;
@@ -811,6 +816,7 @@ __global__ __launch_bounds__(kSipThreads, (M == 8 || (PH && M == 4)) ? 3 : 6) vo
     // tensor's table after them
     __shared__ uint2 tbl[4096];
     __shared__ uint2 sel[16];
+    __shared__ uint32_t wg_done;  // blocks the workgroup's waves have started (progress balance)
     __shared__ uint2 sel2[13 * 16];
     extern __shared__ __align__(16) uint8_t lds_dyn[];
     uint16_t* xs = reinterpret_cast<uint16_t*>(lds_dyn);
@@ -925,6 +931,7 @@ __global__ __launch_bounds__(kSipThreads, (M == 8 || (PH && M == 4)) ? 3 : 6) vo
     // every wave's direct loads into LDS must land before any wave reads:
     // they precede the two stages' 6 loads (raw: 4) in the wave's queue, so
     // vmcnt(6) completes them while the stages stay in flight
+    if (threadIdx.x == 0) wg_done = 0;
     if constexpr (RAW)
         asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
     else
@@ -1122,8 +1129,27 @@ __global__ __launch_bounds__(kSipThreads, (M == 8 || (PH && M == 4)) ? 3 : 6) vo
     // whole rounds of three blocks, then the remainder
     const uint32_t my_units = wv < units ? (units - wv + kSipWaves - 1) / kSipWaves : 0;
     const uint32_t items = my_units * sh.seg_blocks;
+    const uint32_t wg_items = units * sh.seg_blocks;
+    const bool balance = !DEC && wg_items >= kBalanceMinBlocks * kSipWaves;
     uint32_t k = 0;
     for (; k + 3 <= items; k += 3) {
+        if (balance) {
+            // Progress balance: the SIMD's arbiter favours its oldest
+            // waves, and one workgroup's waves otherwise end up to 6 us
+            // apart on a 26 us launch, the CU's loads thinning out as they
+            // finish. A wave more than kBalanceMargin blocks (of the
+            // workgroup's) behind the workgroup's average progress takes
+            // the SIMD first. Scheduling only: the results are unchanged.
+            // (Off for launches of under kBalanceMinBlocks blocks a wave,
+            // where the atomic's round trip before the loads costs more.)
+            uint32_t tot = 0;
+            if (lane == 0) tot = __hip_atomic_fetch_add(&wg_done, 3u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            tot = __builtin_amdgcn_readfirstlane(tot);
+            if (k * wg_items + kBalanceMargin * items < tot * items)
+                __builtin_amdgcn_s_setprio(2);
+            else
+                __builtin_amdgcn_s_setprio(0);
+        }
         sC = load(oC, rC.t);
         uint2 oN = next_offsets();
         SipRef rN = nr;
