@@ -1130,7 +1130,7 @@ __global__ __launch_bounds__(kSipThreads, (M == 8 || (PH && M == 4)) ? 3 : 6) vo
     const uint32_t my_units = wv < units ? (units - wv + kSipWaves - 1) / kSipWaves : 0;
     const uint32_t items = my_units * sh.seg_blocks;
     const uint32_t wg_items = units * sh.seg_blocks;
-    const bool balance = !DEC && wg_items >= kBalanceMinBlocks * kSipWaves;
+    const bool balance = !DEC && M <= 2 && wg_items >= kBalanceMinBlocks * kSipWaves;
     uint32_t k = 0;
     for (; k + 3 <= items; k += 3) {
         if (balance) {
@@ -1141,7 +1141,9 @@ __global__ __launch_bounds__(kSipThreads, (M == 8 || (PH && M == 4)) ? 3 : 6) vo
             // workgroup's) behind the workgroup's average progress takes
             // the SIMD first. Scheduling only: the results are unchanged.
             // (Off for launches of under kBalanceMinBlocks blocks a wave,
-            // where the atomic's round trip before the loads costs more.)
+            // where the atomic's round trip before the loads costs more,
+            // and at M = 4 and 8: no gain measured, and its registers
+            // would spill there.)
             uint32_t tot = 0;
             if (lane == 0) tot = __hip_atomic_fetch_add(&wg_done, 3u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
             tot = __builtin_amdgcn_readfirstlane(tot);
