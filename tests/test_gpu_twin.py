@@ -94,3 +94,28 @@ def test_plain_linear_twin_takes_sips_kernel(cuda):
     x = bf16_tensor(O.f32_to_bf16_bits(rng.standard_normal(4096).astype(np.float32)), cuda)
     print("case twin plain linear", flush=True)
     assert torch.equal(radix_ops.gemv_fused(twin, x, None), radix_ops.gemv_fused(p, x, None))
+
+
+@pytest.mark.parametrize("profile", ["sip", "gulp"])
+def test_twin_matches_on_a_launch_long_enough_for_progress_balance(cuda, profile):
+    """12288 x 4096 at M = 1 and 2: 192 blocks a workgroup, so the sip
+    kernel's waves rebalance their priorities as they go (launches of 12 or
+    more blocks a wave), in the twin as in the compressed kernel; the
+    outputs stay bit for bit equal, and right."""
+    import torch
+
+    from drinkme_amd import radix_ops
+
+    rng = np.random.default_rng(4096 + len(profile))
+    R, C = 12288, 4096
+    bits = finite_bits(rng, (R, C), spread=True)
+    p, twin = _pair(bits, profile, cuda)
+    xb = O.f32_to_bf16_bits(rng.standard_normal((2, C)).astype(np.float32))
+    x = bf16_tensor(xb, cuda)
+    print(f"case twin balanced launch {profile}", flush=True)
+    y = radix_ops.gemv(p, x[0])
+    assert torch.equal(radix_ops.gemv(twin, x[0]), y), "M=1"
+    assert torch.equal(radix_ops.gemv_mc(twin, x), radix_ops.gemv_mc(p, x)), "M=2"
+    ref, bound = O.gemv_f64(bits, O.bf16_bits_to_f32(xb[:1]))
+    yy = y.cpu().numpy().astype(np.float64)
+    assert np.all(np.abs(yy - ref.reshape(yy.shape)) <= bound.reshape(yy.shape))
