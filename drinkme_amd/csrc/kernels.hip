@@ -342,10 +342,8 @@ constexpr int kSipThreads = kSipWaves * kWave;
 // misses) and only adds dispatch and setup: one per CU measured 2% faster
 // on the Qwen3-8B step and 12% on 4096 x 4096 GEMVs. gulp: two, as its
 // decode is bound by instruction latency and needs the waves. The decode
-// mode (2 KB stored per block): two, measured 3-11% faster than one. A sip
-// launch of at least kSipTwoPerCuBlocks blocks per CU also takes two: at
-// 2374 per CU (Qwen3-8B's lm_head) one was 3% slower.
-constexpr uint32_t kSipPerCu = 1, kGulpPerCu = 2, kDecodePerCu = 2, kSipTwoPerCuBlocks = 1500;
+// mode (2 KB stored per block): two, measured 3-11% faster than one.
+constexpr uint32_t kSipPerCu = 1, kGulpPerCu = 2, kDecodePerCu = 2;
 // The sip kernel's progress balance (below): a margin of 12 measured best
 // of 0, 6, 12, 24 and 48; on for launches of 12 or more blocks a wave (the
 // Qwen3-8B step 1.9% faster than without, one layer 2.6%, 4096 x 4096
@@ -1929,8 +1927,6 @@ bool plan_launch(SipShape& sh, const SipGroup& g, uint32_t n, uint32_t min_rows,
                  uint32_t max_per_cu, bool mf, size_t fixed, bool allow_two, uint32_t& grid_out, size_t& lds_out,
                  bool& two_out) {
     const uint32_t cus = (uint32_t)cu_count();
-    // (a launch of many blocks per CU, such as lm_head, keeps two)
-    if (max_per_cu == 1 && (uint64_t)sh.rows * sh.nb >= (uint64_t)kSipTwoPerCuBlocks * cus) max_per_cu = 2;
     for (uint32_t per_cu = M == 8 ? 1 : max_per_cu; per_cu >= 1; --per_cu) {
         uint32_t grid = std::min<uint32_t>(sh.rows, cus * per_cu);
         uint32_t T = (sh.rows + grid - 1) / grid;
