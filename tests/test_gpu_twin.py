@@ -8,8 +8,9 @@ one launch plan the two outputs are identical.
 Covered: every profile (sip and gulp on their fast kernels, balanced on the
 generic one), M = 1..8, fp32 and bf16 outputs, the fused bias epilogue, a
 row long enough for column phases at M = 8, columns that are not a whole
-number of blocks (the generic kernel at every profile), and an fp32
-activation (the generic kernel's widening path).
+number of blocks (the generic kernel at every profile), an fp32
+activation (the generic kernel's widening path), and a 12288 x 4096
+launch long enough for the sip kernel's progress balance.
 """
 
 import zlib
