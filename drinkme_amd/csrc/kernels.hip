@@ -907,8 +907,9 @@ __global__ __launch_bounds__(kSipThreads, (M == 8 || (PH && M == 4)) ? 3 : 6) vo
     SipStage sB = load(oB, rB.t);
     __builtin_amdgcn_sched_barrier(0);
     // M >= 4 keeps three blocks in flight through its longer per-block work
-    // (measured 2.5-3.7% faster on a Qwen3-8B layer at M = 4; at M = 1 the
-    // same pipeline was 1.7% slower on the step and 6% on 4096 x 4096)
+    // (measured 2-4% faster on Qwen3-8B and 32B-class layers at M = 4 over
+    // two A/B runs; at M = 1 the same pipeline was 1.7% slower on the step
+    // and 6% on 4096 x 4096; at M = 2, mixed)
     constexpr bool DEEP = M >= 4;
     SipStage sC;
     if constexpr (DEEP) {
