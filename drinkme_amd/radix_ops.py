@@ -39,15 +39,22 @@ def _stream():
 
 
 def descriptor(p: dict) -> _native.RadixTensor:
-    """The dmx_radix_tensor of a runtime dict (built once, kept in the dict)."""
-    t = p.get("_dmx")
+    """The dmx_radix_tensor of a runtime dict, kept in the dict with the
+    buffer addresses and sizes it was built from: a copy of the dict with
+    another buffer in it (dict(p, rx_data=...)) gets a descriptor of its
+    own."""
+    sched = p.get("rx_schedule")
+    key = (p["rx_data"].data_ptr(), p["rx_offsets"].data_ptr(), p["rx_palette"].data_ptr(),
+           sched.data_ptr() if sched is not None and sched.numel() else 0, int(p["NW"]), int(p["rx_pad_words"]),
+           int(p["R"]), int(p["C"]), int(p["block_size"]), tuple(int(w) for w in p["widths"]))
+    cached = p.get("_dmx")
+    t = cached[1] if cached is not None and cached[0] == key else None
     if t is None:
         widths = [int(w) for w in p["widths"]]
         t = _native.RadixTensor()
         t.data = p["rx_data"].data_ptr()
         t.offsets = p["rx_offsets"].data_ptr()
         t.palette = p["rx_palette"].data_ptr()
-        sched = p.get("rx_schedule")
         t.schedule = sched.data_ptr() if sched is not None and sched.numel() else None
         t.payload_words = int(p["NW"])
         t.pad_words = int(p["rx_pad_words"])
@@ -55,7 +62,7 @@ def descriptor(p: dict) -> _native.RadixTensor:
         t.n_widths = len(widths)
         for i, w in enumerate(widths):
             t.widths[i] = w
-        p["_dmx"] = t
+        p["_dmx"] = (key, t)
     return t
 
 

@@ -74,3 +74,78 @@ def u16_of(t) -> np.ndarray:
     import torch
 
     return t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def gemv_f64_rows(bits: np.ndarray, xf: np.ndarray, threads: int = 16):
+    """The oracle's float64 dot and bound over row ranges on host threads
+    (its C loop runs outside the GIL): (y, bound) float64 [M, R]."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    xf = np.ascontiguousarray(np.atleast_2d(xf), dtype=np.float32)
+    R = bits.shape[0]
+    y = np.empty((xf.shape[0], R), np.float64)
+    bound = np.empty_like(y)
+    step = max(1, -(-R // (4 * threads)))
+
+    def job(r0):
+        yy, bb = O.gemv_f64(bits[r0:r0 + step], xf)
+        y[:, r0:r0 + step] = yy
+        bound[:, r0:r0 + step] = bb
+
+    with ThreadPoolExecutor(threads) as ex:
+        list(ex.map(job, range(0, R, step)))
+    return y, bound
+
+
+def gemv_f32_rows(bits: np.ndarray, xf: np.ndarray, threads: int = 16) -> np.ndarray:
+    """The oracle's decode-then-matmul (fp32 accumulate) over row ranges on
+    host threads: fp32 [M, R]."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    xf = np.ascontiguousarray(np.atleast_2d(xf), dtype=np.float32)
+    R = bits.shape[0]
+    y = np.empty((xf.shape[0], R), np.float32)
+    step = max(1, -(-R // (4 * threads)))
+
+    def job(r0):
+        y[:, r0:r0 + step] = O.gemv_f32(bits[r0:r0 + step], xf)
+
+    with ThreadPoolExecutor(threads) as ex:
+        list(ex.map(job, range(0, R, step)))
+    return y
+
+
+def planted_mistakes_rejected(y_row: np.ndarray, bits: np.ndarray, xf_row: np.ndarray, r: int) -> list:
+    """The bound check's negative controls, planted in the oracle (CPU):
+    for output row r of a result y_row (float, [R]) that passes the check,
+    three plausible decoder or indexing mistakes must each fail it:
+      - one weight's exponent off by one (bit 7 flipped) at the row's
+        largest |x w| term (a wrong palette or table entry);
+      - that term dropped (a lost weight);
+      - the neighbouring row's sums compared (a row index off by one).
+    Returns the three err/bound ratios (each must exceed 1), or None when
+    the row's largest term is within twice its bound: a single term that
+    small sits under the bound's absolute floor and no check of that bound
+    can see it."""
+    xf_row = np.asarray(xf_row, np.float32).reshape(1, -1)
+    row = np.ascontiguousarray(bits[r:r + 1])
+    w = O.bf16_bits_to_f32(row).astype(np.float64)
+    terms = np.abs(w * xf_row.astype(np.float64))
+    c = int(np.argmax(terms))
+    y = float(y_row[r])
+    if terms[0, c] <= 2.0 * O.gemv_f64(row, xf_row)[1][0, 0]:
+        return None
+    out = []
+    flipped = row.copy()
+    flipped[0, c] ^= np.uint16(1 << 7)
+    ref, bound = O.gemv_f64(flipped, xf_row)
+    out.append(abs(y - ref[0, 0]) / bound[0, 0])
+    dropped = row.copy()
+    dropped[0, c] &= np.uint16(0x8000)  # that weight as a signed zero: its term gone
+    ref, bound = O.gemv_f64(dropped, xf_row)
+    out.append(abs(y - ref[0, 0]) / bound[0, 0])
+    other = r + 1 if r + 1 < bits.shape[0] else r - 1
+    if other >= 0:
+        ref, bound = O.gemv_f64(np.ascontiguousarray(bits[other:other + 1]), xf_row)
+        out.append(abs(y - ref[0, 0]) / bound[0, 0])
+    return out
