@@ -33,7 +33,9 @@ Reported:
               its launches
   cpu_baseline  drinkme's CPU route on the host's cores: the compiled
               drinkme decoder (oracle/_ref) + torch F.linear, on a bounded
-              sample (layer 0), scaled to the step by weight count
+              sample (layer 0), scaled to the step by weight count; three
+              legs (all host threads, one thread, and F.linear over the
+              cached decoded weight), `value` the all-threads leg
 One JSON line goes to stdout; progress lines go to stderr.
 """
 
@@ -122,13 +124,20 @@ def time_graph(fn, replays: int, warmup: int) -> float:
     return start.elapsed_time(end) / replays
 
 
-def cpu_baseline(tensors, xs, budget_s: float = 12.0):
+def cpu_baseline(tensors, xs, budget_s: float = 10.0):
     """drinkme's CPU route (src/drinkme/codec/swap.py:344-352): decode the
     weight with drinkme's compiled C++ decoder (oracle/_ref; the oracle's C
     decoder when that library is absent), then torch F.linear on the bf16
-    weight. Row ranges decode on all host threads. Sample: layer 0's seven
-    tensors, repeated within `budget_s`; scaled to the whole step by
-    weight count."""
+    weight. Three legs, each on a bounded sample of the workload and scaled
+    to the whole sweep by weight count:
+      all_cores   decode on every host thread (up to 16, over row ranges) +
+                  F.linear on as many; per call (value is this leg's rate)
+      one_thread  decode and F.linear on one thread: the serve route's own
+                  decode runs single-threaded (radix_native.py:221, called
+                  without workers from radix_pack.py:292-294)
+      cached_w    F.linear alone over the already-decoded weight, every
+                  thread: the CPU route after its first call, which keeps
+                  the decoded weight (swap.py:350-351)"""
     from concurrent.futures import ThreadPoolExecutor
 
     import numpy as np
@@ -138,7 +147,6 @@ def cpu_baseline(tensors, xs, budget_s: float = 12.0):
 
     kind = "reference" if O.ref_available() else "port"
     threads = min(os.cpu_count() or 1, 16)
-    torch.set_num_threads(threads)
     sample = [t for t in tensors if t["layer"] == tensors[0]["layer"]]
     host = []
     for t in sample:
@@ -146,38 +154,67 @@ def cpu_baseline(tensors, xs, budget_s: float = 12.0):
         host.append((rt["rx_palette_np"], rt["rx_offsets"].cpu().numpy(),
                      rt["rx_data"][: rt["NW"]].cpu().numpy(), t["R"], t["C"], tuple(rt["widths"])))
     xcpu = {c: x.cpu() for c, x in xs.items()}
+    total_w = sum(t["R"] * t["C"] for t in tensors)
+    total_bytes = sum(t["bytes"] for t in tensors)
 
-    def decode_gemv(h):
+    def decode(h, nthreads):
         pal, off, data, R, C, widths = h
         out = np.empty((R, C), np.uint16)
-        step = -(-R // (4 * threads))
+        step = -(-R // (4 * nthreads)) if nthreads > 1 else R
         if kind == "reference":
             job = lambda r: O.ref_decode(pal, off, data, R, C, widths, r, min(step, R - r), out[r:])  # noqa: E731
         else:
             pk = O.Pack((R, C), 1024, widths, pal, off, data)
             job = lambda r: O.decode_rows(pk, r, min(step, R - r), out[r:])  # noqa: E731
-        with ThreadPoolExecutor(threads) as ex:
-            list(ex.map(job, range(0, R, step)))
-        W = torch.from_numpy(out.view(np.int16)).view(torch.bfloat16)
-        return torch.nn.functional.linear(xcpu[C], W)
+        if nthreads > 1:
+            with ThreadPoolExecutor(nthreads) as ex:
+                list(ex.map(job, range(0, R, step)))
+        else:
+            job(0)
+        return torch.from_numpy(out.view(np.int16)).view(torch.bfloat16)
 
-    reps, t0 = 0, time.time()
-    while True:
-        for h in host:
-            decode_gemv(h)
-        reps += 1
-        if time.time() - t0 > budget_s or reps >= 20:
-            break
-    per_sample = (time.time() - t0) / reps
-    sample_w = sum(t["R"] * t["C"] for t in sample)
-    total_w = sum(t["R"] * t["C"] for t in tensors)
-    step_s = per_sample * total_w / sample_w
-    total_bytes = sum(t["bytes"] for t in tensors)
-    return {"value": total_bytes / step_s / 1e9, "unit": "GB/s", "cores": threads, "kind": kind,
-            "sample": f"layer {sample[0]['layer']} ({len(sample)} tensors, {sample_w / 1e6:.0f} M weights) "
-                      f"x{reps}: decode (drinkme C++ decoder, {threads} threads over row ranges) + torch "
-                      f"F.linear bf16 per call; scaled by weight count to the step",
-            "ms_per_step": step_s * 1e3}
+    def timed(fn, items, budget, max_reps=20):
+        """Seconds per pass over `items` (whole passes within the budget, at
+        least one), and the passes made. A pass stops early when one item
+        alone exceeds the budget: then the weights it covered are returned."""
+        reps, t0, covered = 0, time.time(), 0
+        while True:
+            covered = 0
+            for h in items:
+                fn(h)
+                covered += h[3] * h[4]
+                if reps == 0 and time.time() - t0 > budget:
+                    break
+            reps += 1
+            if time.time() - t0 > budget or reps >= max_reps:
+                break
+        return (time.time() - t0) / reps, reps, covered
+
+    def leg(name, per_pass_s, weights, reps, cores, what):
+        step_s = per_pass_s * total_w / weights
+        return {"value": total_bytes / step_s / 1e9, "unit": "GB/s", "cores": cores, "ms_per_step": step_s * 1e3,
+                "sample": f"{what}: {weights / 1e6:.1f} M weights of layer {sample[0]['layer']} x{reps}, "
+                          f"scaled by weight count to the sweep ({total_w / 1e9:.3f} G weights)"}
+
+    legs = {}
+    torch.set_num_threads(threads)
+    per, reps, w = timed(lambda h: torch.nn.functional.linear(xcpu[h[4]], decode(h, threads)), host, budget_s)
+    legs["all_cores"] = leg("all_cores", per, w, reps, threads,
+                            f"decode (drinkme C++ decoder, {threads} threads over row ranges) + torch F.linear "
+                            f"bf16 ({threads} threads) per call")
+    torch.set_num_threads(1)
+    per, reps, w = timed(lambda h: torch.nn.functional.linear(xcpu[h[4]], decode(h, 1)), host, 0.8 * budget_s, 1)
+    legs["one_thread"] = leg("one_thread", per, w, reps, 1,
+                             "decode (drinkme C++ decoder, one thread) + torch F.linear bf16 (one thread) per call")
+    torch.set_num_threads(threads)
+    weights = [(decode(h, threads), h[4]) for h in host]
+    per, reps, w = timed(lambda wc: torch.nn.functional.linear(xcpu[wc[1]], wc[0]),
+                         [(W, C, 0, W.shape[0], W.shape[1]) for W, C in weights], 0.4 * budget_s)
+    legs["cached_w"] = leg("cached_w", per, w, reps, threads,
+                           f"torch F.linear bf16 ({threads} threads) over the decoded weight, kept between calls")
+    out = dict(legs["all_cores"])
+    out.update(kind=kind, legs=legs)
+    return out
 
 
 def main() -> int:
@@ -312,7 +349,9 @@ def main() -> int:
     if not args.no_cpu_baseline:
         log("cpu baseline ...")
         cpu = cpu_baseline(tensors, xs)
-        log(f"cpu baseline: {cpu['value']:.2f} GB/s ({cpu['ms_per_step']:.0f} ms per step, {cpu['cores']} threads)")
+        for name, lg in cpu["legs"].items():
+            log(f"cpu baseline {name}: {lg['value']:.3f} GB/s ({lg['ms_per_step']:.0f} ms per sweep, "
+                f"{lg['cores']} thread(s))")
     out = {
         "metric": "compressed-HBM GB/s of the Qwen3-8B decode-step GEMV sweep (sip, M=1)"
         if (args.workload, args.profile, args.m) == ("qwen3-8b-step", "sip", 1)

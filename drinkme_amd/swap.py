@@ -1,28 +1,29 @@
-"""The operator surface over the HIP arms: drinkme's runtime dict
-(to_device_radix, src/drinkme/codec/swap.py:80-161) and the resident
-compressed Linear with its M router and single-rounding epilogue
-(CompressedLinear / RadixCompressedLinear, src/drinkme/codec/swap.py:
-228-456).
+"""The operator surface over the HIP arms, for drinkme's loader and serving
+loop: the resident runtime dict of a packed tensor and the module that
+serves it.
 
-Routes (src/drinkme/codec/swap.py:302-335):
-  M == 1          "gemv"   fused decode + GEMV, bias in fp32, one rounding
-  2 <= M <= 8     "mc"     the same kernel family over M activation rows
-  M >= 9          "dense"  decode the weight once (transient) + F.linear
-  M > 8, dense
-  disabled        "loop"   one M = 1 GEMV per row
-There is no CPU route: the arms run on the GPU and a CPU tensor is refused.
-
-Beside it, the raw bf16 surface that binds the same ops module:
-NarrowLinear / install_narrow (src/drinkme/codec/swap.py:530-627), the
-Linears under the codec's row threshold, through radix_ops.gemv_narrow;
-and to_device_twin (swap.py:168-196), a raw bf16 weight's dict that the
-GEMV calls run through the raw kernel.
+Contract kept from drinkme (src/drinkme/codec/swap.py):
+  - to_device_radix(pack, device) -> the runtime dict (:80-161): rx_data
+    (payload then the reach pad), rx_offsets, rx_palette (padded tier
+    tables), rx_schedule (gulp), rx_palette_np and the scalars;
+  - RadixCompressedLinear(runtime, bias): M activation rows through one of
+    four arms (:302-335, :443-456), the bias added to the fp32 sums before
+    the one rounding to x's dtype (:284-300);
+  - DRINKME_PREFILL_DENSE_MIN, read once: the row count from which the
+    dense arm serves; 0 or less turns it off (:207-224);
+  - NarrowLinear / install_narrow (:530-627) and eligible (:850-854): the
+    raw bf16 Linears under the codec's row threshold, through gemv_narrow;
+  - to_device_twin (:168-196), to_device_raw / RawLinear (:68-77, :459-495)
+    and make_module (:900-919).
+There is no CPU route: every arm runs on the GPU, and an activation on the
+CPU is refused.
 """
 
 from __future__ import annotations
 
 import os
 import warnings
+from dataclasses import dataclass
 
 import numpy as np
 import torch
@@ -31,65 +32,122 @@ from . import radix_ops
 from .radix_pack import ARRAYS_RADIX, block_word_bounds, padded_palette_words, validate_radix
 
 FORMAT_VERSION = 1
-GEMM_MIN_ROWS = radix_ops.MC_MAX + 1  # src/drinkme/codec/swap.py:251
 
-_DENSE_MIN: int | None = None
+# ---------------------------------------------------------------- routing --
+
+ENV_DENSE_MIN = "DRINKME_PREFILL_DENSE_MIN"
 
 
-def _dense_min() -> int:
-    """DRINKME_PREFILL_DENSE_MIN if set (<= 0 disables the dense arm), else
-    GEMM_MIN_ROWS; read once (src/drinkme/codec/swap.py:208-225)."""
-    global _DENSE_MIN
-    if _DENSE_MIN is None:
-        raw = os.environ.get("DRINKME_PREFILL_DENSE_MIN", "").strip()
-        try:
-            _DENSE_MIN = int(raw) if raw else GEMM_MIN_ROWS
-        except ValueError:
-            warnings.warn(f"DRINKME_PREFILL_DENSE_MIN={raw!r} is not an integer; using {GEMM_MIN_ROWS}")
-            _DENSE_MIN = GEMM_MIN_ROWS
-    return _DENSE_MIN
+class RoutePolicy:
+    """Which arm serves M activation rows.
+
+        M == 1                         gemv   the fused decode + GEMV
+        M >= dense_from (> 0)          dense  decode once, then F.linear
+        2 <= M <= MC_MAX otherwise     mc     the same kernels over M rows
+        M > MC_MAX, no dense arm       loop   one M = 1 call per row
+
+    dense_from comes from DRINKME_PREFILL_DENSE_MIN the first time it is
+    asked for (an unparsable value warns and keeps the default, MC_MAX + 1);
+    `override` replaces it, `reset` makes the next call read the environment
+    again."""
+
+    default = radix_ops.MC_MAX + 1
+
+    def __init__(self):
+        self._dense_from: int | None = None
+
+    @property
+    def dense_from(self) -> int:
+        if self._dense_from is None:
+            text = os.environ.get(ENV_DENSE_MIN, "").strip()
+            value = self.default
+            if text:
+                try:
+                    value = int(text)
+                except ValueError:
+                    warnings.warn(f"{ENV_DENSE_MIN}={text!r} is not an integer; using {self.default}")
+            self._dense_from = value
+        return self._dense_from
+
+    def override(self, value: int | None) -> None:
+        self._dense_from = value
+
+    def reset(self) -> None:
+        self._dense_from = None
+
+    def arm(self, m: int) -> str:
+        if m == 1:
+            return "gemv"
+        if 0 < self.dense_from <= m:
+            return "dense"
+        return "mc" if m <= radix_ops.MC_MAX else "loop"
+
+
+ROUTES = RoutePolicy()
+GEMM_MIN_ROWS = RoutePolicy.default  # src/drinkme/codec/swap.py:251
+
+# ------------------------------------------------------------ runtime dict --
+
+
+@dataclass(frozen=True)
+class _Layout:
+    """The device layout of one radix tensor."""
+    rows: int
+    cols: int
+    block: int
+    widths: tuple
+    blocks: int  # rows x blocks per row
+    pad: int     # zero words after the payload: the farthest any block reaches
+
+    @classmethod
+    def of(cls, pack: dict) -> "_Layout":
+        R, C, B = int(pack["R"]), int(pack["C"]), int(pack["block_size"])
+        widths = tuple(int(w) for w in pack["widths"])
+        return cls(R, C, B, widths, R * -(-C // B), int(block_word_bounds(B, widths)[1]))
+
+
+def _upload_u32(arr: np.ndarray, dev: torch.device, extra_zero_words: int = 0) -> torch.Tensor:
+    """A u32 host array on the device, followed by extra_zero_words zeros."""
+    host = np.ascontiguousarray(arr, dtype=np.uint32).reshape(-1)
+    out = torch.empty(host.size + extra_zero_words, dtype=torch.uint32, device=dev)
+    out[:host.size].copy_(torch.from_numpy(host))
+    if extra_zero_words:
+        out[host.size:].zero_()
+    return out
 
 
 def to_device_radix(pack: dict, device="cuda") -> dict:
-    """A radix tensor dict -> device-resident runtime buffers
-    (src/drinkme/codec/swap.py:80-161):
+    """A packed radix tensor (rx_palette, rx_offsets, rx_data + scalars) as
+    device buffers, after the descriptor gate (validate_radix):
 
-      rx_data      u32 [NW + pad]  the block streams, then `pad` zero words
-                                   (block_word_bounds(B)[1]: sip 608, gulp 768)
+      rx_data      u32 [NW + pad]  the block streams, then pad zero words
+                                   (pad = block_word_bounds(B)[1]: sip 608,
+                                   gulp 768): no kernel read of any block
+                                   leaves the allocation
       rx_offsets   u32 [NBK + 1]   the word directory
-      rx_palette   u32 [...]       the padded per-tier lookup tables
-      rx_schedule  u16 [NBK]       > 2 tiers: the per-block tier stream
-                                   lengths, prepared on the device; else empty
-    The descriptors pass the gate (validate_radix) before any allocation."""
+      rx_palette   u32 [...]       each nonterminal tier's entries, padded
+                                   with zero bytes to whole words
+      rx_schedule  u16 [NBK]       more than two tiers: each block's tier
+                                   stream lengths, computed on the device
+                                   (dmx_radix_prepare); else empty
+    The remaining scalars of the pack dict are kept."""
     validate_radix(pack)
     dev = torch.device(device)
     if dev.type != "cuda":
         raise ValueError("to_device_radix: the radix arms run on the GPU")
-    R, C = int(pack["R"]), int(pack["C"])
-    widths = tuple(int(w) for w in pack["widths"])
-    B = int(pack["block_size"])
-    nblk = R * ((C + B - 1) // B)
-    payload = np.ascontiguousarray(pack["rx_data"], dtype=np.uint32).reshape(-1)
-    pad = int(block_word_bounds(B, widths)[1])
-    data = torch.zeros(payload.size + pad, dtype=torch.uint32, device=dev)
-    data[: payload.size].copy_(torch.from_numpy(payload))
-    offsets = torch.from_numpy(np.ascontiguousarray(pack["rx_offsets"], dtype=np.uint32)).to(dev)
-    palette = torch.from_numpy(padded_palette_words(pack["rx_palette"], widths).copy()).to(dev)
-    if len(widths) > 2:
-        schedule = radix_ops.prepare_schedule(data, offsets, C, widths, B, nblk)
-    else:
-        schedule = torch.empty(0, dtype=torch.uint16, device=dev)
-    return {
-        **{k: v for k, v in pack.items() if k not in ARRAYS_RADIX},
-        "rx_data": data,
-        "rx_offsets": offsets,
-        "rx_palette": palette,
-        "rx_schedule": schedule,
-        "rx_palette_np": np.ascontiguousarray(pack["rx_palette"], dtype=np.uint8),
-        "NW": int(payload.size), "rx_pad_words": pad,
-        "R": R, "C": C, "widths": widths, "block_size": B, "NBK": nblk,
-        "codec": "radix", "format_version": FORMAT_VERSION, "layout": 0,
-    }
+    lay = _Layout.of(pack)
+    payload_words = int(np.asarray(pack["rx_data"]).size)
+    data = _upload_u32(pack["rx_data"], dev, lay.pad)
+    offsets = _upload_u32(pack["rx_offsets"], dev)
+    tables = _upload_u32(padded_palette_words(pack["rx_palette"], lay.widths), dev)
+    schedule = (radix_ops.prepare_schedule(data, offsets, lay.cols, lay.widths, lay.block, lay.blocks)
+                if len(lay.widths) > 2 else torch.empty(0, dtype=torch.uint16, device=dev))
+    runtime = {k: v for k, v in pack.items() if k not in ARRAYS_RADIX}
+    runtime.update(rx_data=data, rx_offsets=offsets, rx_palette=tables, rx_schedule=schedule,
+                   rx_palette_np=np.ascontiguousarray(pack["rx_palette"], dtype=np.uint8),
+                   NW=payload_words, rx_pad_words=lay.pad, R=lay.rows, C=lay.cols, widths=lay.widths,
+                   block_size=lay.block, NBK=lay.blocks, codec="radix", format_version=FORMAT_VERSION, layout=0)
+    return runtime
 
 
 def resident_bytes(p: dict) -> int:
@@ -98,10 +156,43 @@ def resident_bytes(p: dict) -> int:
     return sum(p[k].numel() * p[k].element_size() for k in ("rx_data", "rx_offsets", "rx_palette", "rx_schedule"))
 
 
+def to_device_twin(w_bf16, widths=(3, 8), device: str = "cuda") -> dict:
+    """A raw bf16 weight [R, C] as a twin dict: the weight resident,
+    row-major, codec "twin", with the widths of the compressed tensor it
+    stands beside. The GEMV calls of radix_ops run it through that tensor's
+    kernel, the decode replaced by a load of the raw weight."""
+    w = w_bf16.detach()
+    if w.dtype != torch.bfloat16:
+        raise TypeError(f"to_device_twin: {w.dtype} is not bf16")
+    rows, cols = (int(n) for n in w.shape)
+    return {"weight": w.contiguous().to(torch.device(device)), "R": rows, "C": cols,
+            "widths": tuple(int(v) for v in widths), "block_size": 1024, "NBK": rows * -(-cols // 1024),
+            "codec": "twin", "layout": 0}
+
+
+def to_device_raw(pack: dict, device: str = "cuda") -> dict:
+    """A tensor stored raw (radix would have expanded it: codec "raw", its
+    bf16 bits as raw_bits) as its resident bf16 weight."""
+    rows, cols = int(pack["R"]), int(pack["C"])
+    bits = np.ascontiguousarray(pack["raw_bits"], dtype=np.uint16).reshape(rows, cols)
+    weight = torch.from_numpy(bits.view(np.int16).copy()).view(torch.bfloat16).to(torch.device(device))
+    return {"weight": weight, "R": rows, "C": cols, "codec": "raw", "format_version": FORMAT_VERSION, "layout": 0}
+
+
+# ----------------------------------------------------------------- modules --
+
+
 class RadixCompressedLinear(torch.nn.Module):
-    """A radix-coded Linear resident on the GPU: the M router, the arms and
-    the fp32-accumulate-then-round-once epilogue of drinkme's
-    RadixCompressedLinear (src/drinkme/codec/swap.py:384-456)."""
+    """A radix-coded Linear resident on the GPU (`p` is its runtime dict).
+
+    forward(x [..., C]) -> [..., R] in x's dtype. Each arm accumulates in
+    fp32 and adds the bias to the fp32 sums before the only rounding:
+      gemv, mc   one launch of radix_ops.gemv_rows for bf16 or fp32 x (bias
+                 and rounding in the kernel); other dtypes go through fp32
+                 rows and round here
+      dense      the weight decoded once (a transient bf16 tensor), then
+                 F.linear(x, W, bias): stock's own arithmetic
+      loop       one single-row call per activation row"""
 
     GEMM_MIN_ROWS = GEMM_MIN_ROWS
 
@@ -114,22 +205,17 @@ class RadixCompressedLinear(torch.nn.Module):
         self.R, self.C = int(runtime["R"]), int(runtime["C"])
         self.tensor_codec = "radix"
         self.layout = 0
+        self._arms = {"gemv": self._rows_arm, "mc": self._rows_arm, "dense": self._dense_arm,
+                      "loop": self._loop_arm}
 
     def _route(self, x) -> str:
-        if x.device.type == "cpu":
-            return "cpu"
-        return self._route_rows(x.numel() // x.shape[-1])
+        """The arm for x: "cpu" off the GPU, else by its row count (the
+        product of its leading dimensions)."""
+        return "cpu" if x.device.type == "cpu" else self._route_rows(x.numel() // x.shape[-1])
 
     @staticmethod
     def _route_rows(m: int) -> str:
-        if m == 1:
-            return "gemv"
-        dense_min = _dense_min()
-        if 0 < dense_min <= m:
-            return "dense"
-        if m <= radix_ops.MC_MAX:
-            return "mc"
-        return "loop"
+        return ROUTES.arm(m)
 
     def forward(self, x):
         return self._forward(x, self._route(x))
@@ -137,107 +223,124 @@ class RadixCompressedLinear(torch.nn.Module):
     def _forward(self, x, route: str):
         if route == "cpu":
             raise RuntimeError("RadixCompressedLinear: the radix arms run on the GPU; x is on the CPU")
-        shape = x.shape
-        xf = x.reshape(-1, self.C)
-        if route in ("gemv", "mc") and x.dtype in (torch.bfloat16, torch.float32):
-            # one launch: fp32 accumulation, the bias in fp32, one rounding to x.dtype
-            out = radix_ops.gemv_rows(self.p, xf, self.bias, x.dtype)
-            return out.reshape(*shape[:-1], self.R)
-        if route == "dense":
-            W = radix_ops.decode_weight(self.p)
-            out = torch.nn.functional.linear(xf.to(W.dtype) if xf.dtype != W.dtype else xf, W, self.bias)
-            return out.to(x.dtype).reshape(*shape[:-1], self.R)
-        # other dtypes through fp32 rows, or the per-row loop
-        rows = xf.shape[0]
-        outs = torch.empty(rows, self.R, device=x.device, dtype=torch.float32)
-        step = 1 if route == "loop" else rows
-        for i in range(0, rows, step):
-            outs[i:i + step] = radix_ops.gemv_rows(self.p, xf[i:i + step].float(), None, torch.float32)
-        if self.bias is not None:
-            outs = outs + self.bias
-        return outs.to(x.dtype).reshape(*shape[:-1], self.R)
+        rows = x.reshape(-1, self.C)
+        y = self._arms[route](rows, x.dtype)
+        return y.reshape(*x.shape[:-1], self.R)
+
+    def _round_once(self, y32: torch.Tensor, dtype) -> torch.Tensor:
+        """fp32 sums -> + bias in fp32 -> one rounding to dtype."""
+        return (y32 if self.bias is None else y32 + self.bias).to(dtype)
+
+    def _rows_arm(self, rows, dtype):
+        if dtype in (torch.bfloat16, torch.float32):
+            return radix_ops.gemv_rows(self.p, rows, self.bias, dtype)
+        return self._round_once(radix_ops.gemv_rows(self.p, rows.float(), None, torch.float32), dtype)
+
+    def _dense_arm(self, rows, dtype):
+        weight = radix_ops.decode_weight(self.p)
+        return torch.nn.functional.linear(rows if rows.dtype == weight.dtype else rows.to(weight.dtype), weight,
+                                          self.bias).to(dtype)
+
+    def _loop_arm(self, rows, dtype):
+        sums = torch.empty(rows.shape[0], self.R, device=rows.device, dtype=torch.float32)
+        for i in range(rows.shape[0]):
+            sums[i:i + 1] = radix_ops.gemv_rows(self.p, rows[i:i + 1].float(), None, torch.float32)
+        return self._round_once(sums, dtype)
+
+
+class RawLinear(torch.nn.Module):
+    """A tensor stored raw (to_device_raw): stock's F.linear over the
+    resident bf16 weight on every route."""
+
+    def __init__(self, runtime: dict, bias=None):
+        super().__init__()
+        if runtime.get("codec") != "raw":
+            raise ValueError("RawLinear needs a to_device_raw runtime dict")
+        self.p = runtime
+        self.bias = bias
+        self.R, self.C = int(runtime["R"]), int(runtime["C"])
+        self.tensor_codec = "raw"
+        self.layout = 0
+
+    def forward(self, x):
+        return torch.nn.functional.linear(x, self.p["weight"].to(x.device), self.bias)
 
 
 def make_module(pack: dict, bias=None, device="cuda") -> torch.nn.Module:
-    """The served module for one packed tensor: RadixCompressedLinear over
-    its runtime dict (src/drinkme/codec/swap.py:900-919, radix only)."""
-    if pack.get("codec") != "radix":
-        raise ValueError("make_module: not a radix tensor dict")
-    return RadixCompressedLinear(to_device_radix(pack, device), bias)
+    """The served module of one packed tensor, by its codec: radix ->
+    RadixCompressedLinear over to_device_radix, raw -> RawLinear."""
+    kinds = {"radix": (RadixCompressedLinear, to_device_radix), "raw": (RawLinear, to_device_raw)}
+    codec = pack.get("codec")
+    if codec not in kinds:
+        raise ValueError(f"make_module: codec {codec!r} is not a radix or raw tensor")
+    module, resident = kinds[codec]
+    return module(resident(pack, device), bias)
+
+
+# ------------------------------------------------------- the raw Linears --
 
 
 def eligible(child) -> bool:
-    """A Linear the codec takes (src/drinkme/codec/swap.py:850-854): bf16,
-    C % 4 == 0, both dims >= 1024."""
+    """A Linear the codec packs: bf16, columns a multiple of 4, both
+    dimensions at least 1024."""
     if not isinstance(child, torch.nn.Linear):
         return False
-    w = child.weight.data
-    return w.dtype == torch.bfloat16 and w.shape[1] % 4 == 0 and min(w.shape) >= 1024
+    rows, cols = child.weight.shape
+    return child.weight.dtype == torch.bfloat16 and cols % 4 == 0 and min(rows, cols) >= 1024
 
 
 class NarrowLinear(torch.nn.Linear):
-    """A raw bf16 Linear under the codec's row threshold, served by the raw
-    GEMV (src/drinkme/codec/swap.py:530-610): M <= 8 rows in one launch of
-    radix_ops.gemv_narrow (fp32 accumulate, the bias added in fp32, one
-    rounding); more rows, or a CPU tensor, is F.linear. The weight and bias
-    are the adopted Linear's own Parameters. Row m of an M-row call is the
-    one-row call bit for bit."""
+    """A bf16 Linear the codec leaves raw because it has fewer than 1024
+    rows, served on the GPU by radix_ops.gemv_narrow for 1..MC_MAX rows
+    (fp32 accumulation, the bias in fp32, one rounding; row m of an M-row
+    call equals the one-row call bit for bit) and by F.linear otherwise.
+    Its weight and bias are the adopted Linear's own Parameters."""
 
-    BLOCK = 512  # drinkme's launch knobs, passed through (swap.py:577-578)
-    NUM_WARPS = 4
-    MAX_ROWS = 1024  # swap.py:581-582
-    MIN_COLS = 1024
+    BLOCK = 512      # launch knobs of drinkme's kernel (swap.py:577-578),
+    NUM_WARPS = 4    # passed through to gemv_narrow, which ignores them
+    MAX_ROWS = 1024  # the largest weight this serves: rows ...
+    MIN_COLS = 1024  # ... and the shortest: columns
 
     @classmethod
     def wants(cls, mod) -> bool:
+        """A plain torch Linear (not a subclass) the codec does not take,
+        with a bf16 GPU weight of at most MAX_ROWS rows and at least
+        MIN_COLS columns, a multiple of 4."""
         if type(mod) is not torch.nn.Linear or eligible(mod):
             return False
         w = mod.weight
-        return (w.dtype == torch.bfloat16 and w.device.type == "cuda" and w.shape[0] <= cls.MAX_ROWS
-                and w.shape[1] >= cls.MIN_COLS and w.shape[1] % 4 == 0)
+        rows, cols = w.shape
+        fits = rows <= cls.MAX_ROWS and cols >= cls.MIN_COLS and cols % 4 == 0
+        return fits and w.dtype == torch.bfloat16 and w.device.type == "cuda"
 
     @classmethod
     def adopt(cls, lin: torch.nn.Linear) -> "NarrowLinear":
-        """The same parameters under this class: no copy."""
-        new = cls(lin.in_features, lin.out_features, bias=lin.bias is not None, device="meta")
-        new.weight = lin.weight
-        new.bias = lin.bias
-        return new
+        """A NarrowLinear holding lin's own weight and bias Parameters: no
+        copy and no new allocation."""
+        mod = cls.__new__(cls)
+        torch.nn.Module.__init__(mod)
+        mod.in_features, mod.out_features = lin.in_features, lin.out_features
+        mod.weight = lin.weight
+        mod.register_parameter("bias", lin.bias)
+        return mod
 
     def forward(self, x):
-        shape = x.shape
-        xm = x.reshape(-1, self.in_features)
-        if xm.shape[0] > radix_ops.MC_MAX or x.device.type != "cuda":
+        rows = x.reshape(-1, self.in_features)
+        if x.device.type != "cuda" or rows.shape[0] > radix_ops.MC_MAX:
             return torch.nn.functional.linear(x, self.weight, self.bias)
-        y = radix_ops.gemv_narrow(self.weight, xm, self.bias, self.BLOCK, self.NUM_WARPS)
-        return y.reshape(*shape[:-1], self.out_features)
+        y = radix_ops.gemv_narrow(self.weight, rows, self.bias, self.BLOCK, self.NUM_WARPS)
+        return y.reshape(*x.shape[:-1], self.out_features)
 
 
 def install_narrow(model, device: str) -> list:
-    """Every raw Linear NarrowLinear.wants, adopted in place; returns the
-    (name, (R, C)) list (src/drinkme/codec/swap.py:613-627). Nothing off
-    the GPU."""
+    """Replaces, in place, every child Linear of `model` that
+    NarrowLinear.wants by its adopted NarrowLinear; returns [(qualified
+    name, (R, C))]. Nothing is replaced off the GPU."""
     if not str(device).startswith("cuda"):
         return []
-    done = []
-    for parent_name, parent in list(model.named_modules()):
-        for child_name, child in list(parent.named_children()):
-            if NarrowLinear.wants(child):
-                setattr(parent, child_name, NarrowLinear.adopt(child))
-                name = f"{parent_name}.{child_name}" if parent_name else child_name
-                done.append((name, tuple(child.weight.shape)))
-    return done
-
-
-def to_device_twin(w_bf16, widths=(3, 8), device: str = "cuda") -> dict:
-    """A raw bf16 weight [R, C] as a twin dict (src/drinkme/codec/swap.py:
-    168-196): the weight resident and row-major, codec "twin". The GEMV
-    calls of radix_ops run it through the raw kernel."""
-    w = w_bf16.detach()
-    if w.dtype != torch.bfloat16:
-        raise TypeError(f"to_device_twin: {w.dtype} is not bf16")
-    R, C = int(w.shape[0]), int(w.shape[1])
-    B = 1024
-    return {"weight": w.contiguous().to(torch.device(device)), "R": R, "C": C,
-            "widths": tuple(int(x) for x in widths), "block_size": B, "NBK": R * ((C + B - 1) // B),
-            "codec": "twin", "layout": 0}
+    found = [(f"{prefix}.{name}" if prefix else name, parent, name, child)
+             for prefix, parent in model.named_modules() for name, child in parent.named_children()
+             if NarrowLinear.wants(child)]
+    for _, parent, name, child in found:
+        setattr(parent, name, NarrowLinear.adopt(child))
+    return [(qual, tuple(child.weight.shape)) for qual, _, _, child in found]

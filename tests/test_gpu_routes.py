@@ -59,7 +59,7 @@ def test_loop_route_when_the_dense_arm_is_disabled(module, monkeypatch):
     mod, W, bias, rng, torch = module
     from drinkme_amd import swap
 
-    monkeypatch.setattr(swap, "_DENSE_MIN", 0)
+    monkeypatch.setattr(swap.ROUTES, "_dense_from", 0)
     x = torch.from_numpy(rng.standard_normal((12, 2048)).astype(np.float32)).to(W.device).to(torch.bfloat16)
     assert mod._route(x) == "loop"
     y = mod(x)
