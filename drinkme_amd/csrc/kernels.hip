@@ -37,8 +37,11 @@
 #include <numeric>
 
 #include "dmx_radix.h"
+#include "plan.h"
 
 namespace {
+
+using namespace dmx;
 
 constexpr int kWave = 64;
 
@@ -334,24 +337,13 @@ __global__ __launch_bounds__(kGenThreads) void k_gemv_generic(Desc d, const void
 // of the group) in its pair's exponent field. Otherwise (dense escapes, not
 // seen in trained weights) each group's four bytes are read from memory.
 
-constexpr int kSipWaves = 12;
+constexpr int kSipWaves = (int)kPlanWaves;
 constexpr int kSipThreads = kSipWaves * kWave;
-// Resident workgroups per CU that the plans aim for. sip: one. Its loads
-// fill the CU's memory path with 12 waves; a second workgroup starts
-// behind the first (its activation loads queue behind the first's payload
-// misses) and only adds dispatch and setup: one per CU measured 2% faster
-// on the Qwen3-8B step and 12% on 4096 x 4096 GEMVs. gulp: two, as its
-// decode is bound by instruction latency and needs the waves. The decode
-// mode (2 KB stored per block): two, measured 3-11% faster than one.
-constexpr uint32_t kSipPerCu = 1, kGulpPerCu = 2, kDecodePerCu = 2;
 // The sip kernel's progress balance (below): a margin of 12 measured best
 // of 0, 6, 12, 24 and 48; on for launches of 12 or more blocks a wave (the
 // Qwen3-8B step 1.9% faster than without, one layer 2.6%, 4096 x 4096
 // GEMVs unchanged, which were 4-6% slower with it on).
 constexpr uint32_t kBalanceMargin = 12, kBalanceMinBlocks = 12;
-constexpr uint32_t kSipFixed = 256 + 96;  // literal plane + tier 0 words of a 1024-weight block
-constexpr uint32_t kTableBytes = 4096 * 8;
-constexpr uint32_t kSelBytes = (16 + 13 * 16) * 8;
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) void* lds_ptr;
@@ -476,12 +468,6 @@ __device__ __forceinline__ void mf_unit_end(f32x4 (&d)[M], float* out, uint32_t 
     for (int k = 0; k < M; ++k) d[k] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 }
 
-// Verify rows go to the matrix cores where that is faster: sip at M = 4 and
-// 8, gulp at M = 8. Gulp at M = 4 keeps v_dot2: its accumulators would take
-// it past the 80 registers of 6 waves per SIMD, and the decode, bound by
-// latency, loses more from 5 waves than the products gain.
-__host__ __device__ constexpr bool sip_mfma(int M) { return M >= 4; }
-__host__ __device__ constexpr bool gulp_mfma(int M) { return M >= 8; }
 
 // A group of sip tensors that share the activation (the q/k/v or gate/up
 // projections of a layer) runs as one launch: their rows form one row
@@ -489,8 +475,6 @@ __host__ __device__ constexpr bool gulp_mfma(int M) { return M >= 8; }
 // the group's shortest tensor, so a workgroup's rows span at most two
 // tensors; such a workgroup holds both tensors' exponent tables. One tensor
 // is the group of one.
-constexpr int kGroupMax = 4;
-
 struct SipGroup {
     const uint32_t* data[kGroupMax];
     const uint32_t* offsets[kGroupMax];
@@ -499,25 +483,6 @@ struct SipGroup {
     const void* bias[kGroupMax];
     void* out[kGroupMax];
     uint32_t row0[kGroupMax + 1];  // row0[n] = the group's row count
-};
-
-struct SipShape {
-    uint32_t rows, cols, nb;  // rows of the whole group
-    uint32_t n;               // tensors in the group
-    uint32_t rows_per_wg;     // T
-    uint32_t segs;            // S (segments per row) = phases * psegs
-    uint32_t seg_blocks;      // L = NB / S
-    uint32_t phases;          // P: column phases (1 = every activation column resident in LDS)
-    uint32_t phase_blocks;    // K = NB / P column blocks of activations in LDS at a time
-    uint32_t xrow;            // LDS stride of the activation rows, in bf16: K * 1024, plus 128 / M for the matrix cores
-    uint32_t waves;           // W: waves per workgroup
-    uint32_t psegs;           // segments per phase
-    uint32_t phase_units;     // T * psegs units per phase
-    uint32_t dp, dr, ds;      // a wave's step of W units in a full tile: phases, rows, segments
-    uint32_t tbl2_lds;        // dynamic-LDS byte offset of the second table; 0 = no workgroup spans two tensors
-    uint32_t young_from;      // first workgroup dispatched as a CU's second (~0u: one per CU)
-    uint32_t m;               // activation rows (<= the kernel's M; rows past m are padding)
-    int bias_dtype, out_dtype;
 };
 
 // arr[i] for a wave-uniform i < kGroupMax, by selects (no indexed copy of
@@ -552,12 +517,6 @@ __device__ __forceinline__ uint2 sip_offsets(const uint32_t* offsets, uint32_t b
     return make_uint2(p[0], p[1]);
 }
 
-// Per-lane byte offsets of a block's loads: the lane's 16 literal bytes, its
-// two tier-0 words (48 bits at bit 48l) and word l of the terminal region.
-struct SipLanes {
-    uint32_t lit, t0, term;
-    uint32_t raw;  // raw twin: 32 l, the lane's 16 bf16 weights of a block
-};
 
 typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
 
@@ -621,15 +580,6 @@ __device__ __forceinline__ SipStage raw_load(i32x4 rsrc, uint32_t off, const Sip
 
 #define RAW_WAIT(N, S) asm volatile("s_waitcnt vmcnt(" #N ")" : "+v"(S.lit), "+v"(S.hi))
 
-// A wave's place in its work: block j of the unit, the block's index in its
-// tensor's directory, its column block among the resident activation
-// columns, and which of the workgroup's tensors it belongs to.
-struct SipCursor {
-    uint32_t j, blk, cb, t;
-    uint32_t p, r, sp;  // the unit: column phase, row of the workgroup, segment within the phase
-    uint32_t slot;      // the unit's row partial: row * S + segment
-};
-
 // What a block in flight is, taken from the cursor when its loads are
 // issued (so no second cursor walks behind the loads): its unit's row
 // partial, its column block among the resident activations, its tensor
@@ -639,88 +589,6 @@ struct SipRef {
     uint32_t slot, cb, t, p;  // (decode mode: t is the block's index in its tensor, the output's block)
     bool last;
 };
-
-// The workgroup's blocks in row-major order: [0, split_blocks) are its
-// first tensor's, from that tensor's block a_first; the rest its second
-// tensor's, from block 0. A unit lies within one row, so within one tensor.
-struct SipSpan {
-    uint32_t a_first, split_blocks;
-};
-
-// A wave's walk over its units u = wave, wave + W, ... of the workgroup's
-// units, phase-major: unit (p, r, sp) covers row r's column blocks
-// [(p psegs + sp) L, + L). nrows rows; each phase holds nrows * psegs
-// units. The walk steps by W units with additions only (dp phases, dr
-// rows, ds segments); the divisions happen once per wave.
-struct SipWalk {
-    uint32_t nrows, dp, dr, ds;
-};
-
-__device__ __forceinline__ SipWalk sip_walk(const SipShape& sh, uint32_t nrows) {
-    SipWalk w;
-    w.nrows = nrows;
-    if (nrows == sh.rows_per_wg) {  // every tile but perhaps the last: the host's step
-        w.dp = sh.dp;
-        w.dr = sh.dr;
-        w.ds = sh.ds;
-    } else {
-        const uint32_t pu = nrows * sh.psegs, rem = sh.waves % pu;
-        w.dp = sh.waves / pu;
-        w.dr = rem / sh.psegs;
-        w.ds = rem - w.dr * sh.psegs;
-    }
-    return w;
-}
-
-// Sets the block fields of the cursor's unit.
-template <bool TWO>
-__device__ __forceinline__ void sip_unit(const SipShape& sh, SipCursor& c, const SipSpan& sp) {
-    c.j = 0;
-    const uint32_t seg = c.p * sh.psegs + c.sp;
-    c.slot = c.r * sh.segs + seg;
-    const uint32_t wb = c.r * sh.nb + seg * sh.seg_blocks;
-    c.cb = c.sp * sh.seg_blocks;
-    c.t = TWO && wb >= sp.split_blocks;
-    c.blk = c.t ? wb - sp.split_blocks : sp.a_first + wb;
-}
-
-// The cursor at unit u (< W: a wave's first unit), counted up from unit 0.
-template <bool TWO>
-__device__ __forceinline__ void sip_start(const SipShape& sh, SipCursor& c, uint32_t u, const SipWalk& w,
-                                          const SipSpan& sp) {
-    c.p = c.r = c.sp = 0;
-    for (uint32_t i = 0; i < u; ++i) {
-        if (++c.sp == sh.psegs) {
-            c.sp = 0;
-            if (++c.r == w.nrows) {
-                c.r = 0;
-                ++c.p;
-            }
-        }
-    }
-    sip_unit<TWO>(sh, c, sp);
-}
-
-template <bool TWO>
-__device__ __forceinline__ void sip_next(const SipShape& sh, SipCursor& c, const SipWalk& w, const SipSpan& sp) {
-    if (++c.j == sh.seg_blocks) {
-        c.p += w.dp;
-        c.r += w.dr;
-        c.sp += w.ds;
-        if (c.sp >= sh.psegs) {
-            c.sp -= sh.psegs;
-            ++c.r;
-        }
-        if (c.r >= w.nrows) {
-            c.r -= w.nrows;
-            ++c.p;
-        }
-        sip_unit<TWO>(sh, c, sp);
-    } else {
-        ++c.blk;
-        ++c.cb;
-    }
-}
 
 // Rows 0..M-1 of x, columns [phase K 1024, (phase + 1) K 1024), into LDS
 // by direct loads: row m at xs + m xrow; within each 1024-column block,
@@ -824,31 +692,18 @@ __global__ __launch_bounds__(kSipThreads, (M == 8 || (PH && M == 4)) ? 3 : 6) vo
     uint2* tbl2 = reinterpret_cast<uint2*>(lds_dyn + sh.tbl2_lds);
 
     const uint32_t wv = wave_id(), lane = lane_id();
-    const uint32_t r0 = blockIdx.x * sh.rows_per_wg;
-    const uint32_t nrows = min(sh.rows - r0, sh.rows_per_wg);
+    // the workgroup's tensors: ia holds its first row; rows [split, nrows)
+    // are ib's
+    const WgPlace wp0 = wg_place<TWO>(sh, g.row0, blockIdx.x);
+    const uint32_t nrows = wp0.nrows, ia = wp0.ia, ib = wp0.ib, row_a = wp0.row_a, row_b = wp0.row_b;
+    const uint32_t split = wp0.split, lrow_a = wp0.lrow_a;
+    const SipSpan sp = wp0.sp;
     const uint32_t units = nrows * sh.segs;
-
-    // the workgroup's tensors: ia holds row r0; rows [split, nrows) are ib's
-    uint32_t ia = 0;
-#pragma unroll
-    for (int i = 1; i < kGroupMax; ++i) ia += (uint32_t)i < sh.n && g.row0[i] <= r0;
-    const uint32_t ib = min(ia + 1, sh.n - 1);
-    uint32_t row_a = g.row0[0], row_b = g.row0[1];
-#pragma unroll
-    for (int k = 1; k < kGroupMax; ++k) {
-        row_a = ia == (uint32_t)k ? g.row0[k] : row_a;
-        row_b = ia == (uint32_t)k ? g.row0[k + 1] : row_b;
-    }
-    const uint32_t split = TWO ? min(row_b, r0 + nrows) - r0 : nrows;
     const bool two = TWO && split < nrows;
     const uint32_t* data_a = pick(g.data, ia);
     const uint32_t* data_b = pick(g.data, ib);
     const uint32_t* offsets_a = pick(g.offsets, ia);
     const uint32_t* offsets_b = pick(g.offsets, ib);
-    const uint32_t lrow_a = r0 - row_a;
-    SipSpan sp;
-    sp.a_first = lrow_a * sh.nb;
-    sp.split_blocks = split * sh.nb;
 
     // the activation (its first column phase) goes to LDS by direct loads
     // (no registers staged), first in the queue: small and hot in L2; the
@@ -858,7 +713,7 @@ __global__ __launch_bounds__(kSipThreads, (M == 8 || (PH && M == 4)) ? 3 : 6) vo
     // the first two blocks' loads go out before the tables are built; a
     // cursor past the wave's work reads the workgroup's first block instead
     SipCursor p;
-    const SipWalk wk = sip_walk(sh, nrows);
+    const SipWalk wk = sip_walk<false>(sh, nrows);
     sip_start<TWO>(sh, p, wv, wk, sp);
     // each tensor's payload window: from the workgroup's first block of it
     // (the raw twin: from the workgroup's first row, 512 words a block)
@@ -869,24 +724,20 @@ __global__ __launch_bounds__(kSipThreads, (M == 8 || (PH && M == 4)) ? 3 : 6) vo
     }
     const i32x4 rsrc_a = make_rsrc(RAW ? data_a + (uint64_t)sp.a_first * 512u : data_a + base_a, 0x7FFFFFFFu);
     const i32x4 rsrc_b = make_rsrc(data_b + base_b, 0x7FFFFFFFu);
-    SipLanes ln;
-    ln.lit = 16 * lane;
-    ln.t0 = 1024 + 4 * ((3 * lane) >> 1);
-    ln.term = 4 * (kSipFixed + lane);
-    ln.raw = 32 * lane;
+    const SipLanes ln = sip_lanes(lane);
     SipRef nr;  // the last next_offsets() block
     auto next_offsets = [&]() {
-        const bool live = p.p < sh.phases;
-        nr.t = DEC ? p.blk : TWO && live ? p.t : 0u;
+        const Issue is = sip_issue<TWO>(sh, p, sp);
+        nr.t = DEC ? p.blk : is.t;
         nr.slot = p.slot;
         nr.cb = p.cb;
         nr.p = p.p;
         nr.last = p.j + 1 == sh.seg_blocks;
         uint2 o;
         if constexpr (RAW)  // the block's byte offset from the workgroup's first row
-            o = make_uint2(((live ? p.blk : sp.a_first) - sp.a_first) * 2048u, 0u);
+            o = make_uint2((is.blk - sp.a_first) * 2048u, 0u);
         else
-            o = sip_offsets(TWO && nr.t ? offsets_b : offsets_a, live ? p.blk : sp.a_first);
+            o = sip_offsets(TWO && is.t ? offsets_b : offsets_a, is.blk);
         sip_next<TWO>(sh, p, wk, sp);
         return o;
     };
@@ -1272,12 +1123,6 @@ __global__ __launch_bounds__(kSipThreads, (M == 8 || (PH && M == 4)) ? 3 : 6) vo
 // A block with more than 128 tier-1 escapes, or a lane with more than 8,
 // takes an exact lane-serial path that reads the streams from memory.
 
-constexpr uint32_t kGulpFixed = 256 + 64;  // literal plane + tier 0 words of a 1024-weight block
-constexpr uint32_t kGulpT0Bytes = 256 * 8;
-constexpr uint32_t kGulpX2Words = 40;     // per wave: 128 exponent bytes + a window's overhang
-// static LDS of the sip and gulp kernels (their tables), for the host's plans
-constexpr size_t kSipStaticLds = kTableBytes + kSelBytes;
-constexpr size_t kGulpStaticLds = kGulpT0Bytes + kTableBytes + 13 * 16 * 8 + 16 + kSipWaves * kGulpX2Words * 4;
 
 struct GulpStage {
     u32x4 lit;
@@ -1285,13 +1130,6 @@ struct GulpStage {
     uint32_t start, end, sched;
 };
 
-// Per-lane byte offsets of a gulp block's loads: 16 literal bytes (lit),
-// tier-0 word l and tier-1 word l (w: 4l, plus the streams' constant starts
-// as instruction offsets), tier-2 word l / 4 (t2, from the tier-2 start) and
-// terminal word l (w, from the terminal start).
-struct GulpLanes {
-    uint32_t lit, w, t2;
-};
 
 // The block's five loads through the workgroup's buffer resource (based at
 // its first block), untracked by the compiler as in sip_load; completed by
@@ -1304,7 +1142,7 @@ __device__ __forceinline__ GulpStage gulp_load(i32x4 rsrc, uint32_t base, uint2 
     s.end = o.y;
     s.sched = sched;
     // (a schedule byte past its stream's widest keeps every read in the pad)
-    const uint32_t w1 = min(sched & 0xFFu, 64u), w2 = min(sched >> 8, 128u);
+    const uint32_t w1 = min(sched & 0xFFu, kGulpT1Max), w2 = min(sched >> 8, kGulpT2Max);
     const uint32_t soff = (o.x - base) * 4u;
     const uint32_t soff2 = soff + 4u * (kGulpFixed + w1);
     const uint32_t soff3 = soff2 + 4u * w2;
@@ -1392,44 +1230,29 @@ __global__ __launch_bounds__(kSipThreads, (M == 8 || (PH && M == 4)) ? 3 : 6) vo
     const uint8_t* pal2 = reinterpret_cast<const uint8_t*>(pal2w);
 
     const uint32_t wv = wave_id(), lane = lane_id();
-    const uint32_t r0 = blockIdx.x * sh.rows_per_wg;
-    const uint32_t nrows = min(sh.rows - r0, sh.rows_per_wg);
-    const uint32_t units = nrows * sh.segs;
     // the workgroup's tensor (tiles never span two in this kernel)
-    uint32_t ia = 0;
-#pragma unroll
-    for (int i = 1; i < kGroupMax; ++i) ia += (uint32_t)i < sh.n && g.row0[i] <= r0;
-    uint32_t row_a = g.row0[0], row_n = g.row0[1];
-#pragma unroll
-    for (int k = 1; k < kGroupMax; ++k) {
-        row_a = ia == (uint32_t)k ? g.row0[k] : row_a;
-        row_n = ia == (uint32_t)k ? g.row0[k + 1] : row_n;
-    }
+    const WgPlace wp0 = wg_place<false>(sh, g.row0, blockIdx.x);
+    const uint32_t nrows = wp0.nrows, ia = wp0.ia, row_a = wp0.row_a, row_n = wp0.row_b, lrow = wp0.lrow_a;
+    const SipSpan sp = wp0.sp;
+    const uint32_t units = nrows * sh.segs;
     const uint32_t* data = pick(g.data, ia);
     const uint32_t* offsets = pick(g.offsets, ia);
     const uint32_t* sched = reinterpret_cast<const uint32_t*>(pick(g.schedule, ia));
-    const uint32_t lrow = r0 - row_a;
-    SipSpan sp;
-    sp.a_first = lrow * sh.nb;
-    sp.split_blocks = nrows * sh.nb;
     uint32_t* x2 = x2_all + wv * kGulpX2Words;
 
     // the activation rows (first column phase), as in the sip kernel
     if constexpr (!DEC) load_x_slice<M, TH>(sh, x, xs, 0);
 
     SipCursor p, c;
-    const SipWalk wk = sip_walk(sh, nrows);
+    const SipWalk wk = sip_walk<false>(sh, nrows);
     sip_start<false>(sh, p, wv, wk, sp);
     c = p;
     const uint32_t base = ((const_u32_ptr)offsets)[sp.a_first];
     const i32x4 rsrc = make_rsrc(data + base, 0x7FFFFFFFu);
-    GulpLanes ln;
-    ln.lit = 16 * lane;
-    ln.w = 4 * lane;
-    ln.t2 = 4 * (lane >> 2);
+    const GulpLanes ln = gulp_lanes(lane);
     uint32_t ns = 0;  // the schedule of the last next_offsets() block
     auto next_offsets = [&]() {
-        const uint32_t blk = p.p < sh.phases ? p.blk : sp.a_first;
+        const uint32_t blk = sip_issue<false>(sh, p, sp).blk;
         const uint2 o = sip_offsets(offsets, blk);
         ns = (((const_u32_ptr)sched)[blk >> 1] >> ((blk & 1u) * 16)) & 0xFFFFu;
         sip_next<false>(sh, p, wk, sp);
@@ -1485,7 +1308,7 @@ __global__ __launch_bounds__(kSipThreads, (M == 8 || (PH && M == 4)) ? 3 : 6) vo
     auto process = [&](const GulpStage& s0) {
         if (PH)
             while (cur_phase < c.p) phase_advance();
-        const uint32_t w1 = min(s0.sched & 0xFFu, 64u), w2 = min(s0.sched >> 8, 128u);
+        const uint32_t w1 = min(s0.sched & 0xFFu, kGulpT1Max), w2 = min(s0.sched >> 8, kGulpT2Max);
         const bool has_term = s0.end > s0.start + kGulpFixed + w1 + w2;
         // tier 0
         const uint32_t T0 = s0.t0;
@@ -1948,100 +1771,6 @@ bool sip_eligible(const dmx_radix_tensor* t, const void* x, int x_dtype, uint32_
            t->cols % 1024 == 0 && (reinterpret_cast<uintptr_t>(x) & 15u) == 0;
 }
 
-// One launch of the sip kernel over n tensors of equal cols (already
-// checked). Returns 2 when the group cannot run as one launch (a row tile
-// taller than a tensor, or tables past the LDS), having launched nothing.
-// The work plan of a sip or gulp launch over the group's sh.rows rows:
-// up to max_per_cu workgroups per CU where their LDS fits, else fewer (M = 8's
-// registers allow only one); T rows per workgroup; the fewest column phases P (a
-// divisor of NB) whose activation slice fits in LDS; within a phase, the
-// segments that give the fewest block-times per workgroup (a unit's
-// closing wave sum, one per activation row, costing about a quarter of a
-// block). W is the kernel's waves per workgroup, mf whether its verify rows
-// use the matrix cores (their activation rows get a padded stride), `fixed`
-// its static LDS; a second exponent table is added when a tile spans two tensors (allowed
-// only with `allow_two`). Without it, a group whose tensor boundaries the
-// even tile would cut takes the tile height, from T/2 to 4T, that divides
-// every boundary and puts the fewest rows on the busiest CU (the
-// workgroups beyond the resident ones run as a later round). Returns false,
-// planning nothing, when no plan fits.
-bool plan_launch(SipShape& sh, const SipGroup& g, uint32_t n, uint32_t min_rows, uint32_t M, uint32_t W,
-                 uint32_t max_per_cu, bool mf, size_t fixed, bool allow_two, uint32_t& grid_out, size_t& lds_out,
-                 bool& two_out) {
-    const uint32_t cus = (uint32_t)cu_count();
-    for (uint32_t per_cu = M == 8 ? 1 : max_per_cu; per_cu >= 1; --per_cu) {
-        uint32_t grid = std::min<uint32_t>(sh.rows, cus * per_cu);
-        uint32_t T = (sh.rows + grid - 1) / grid;
-        bool two = false;
-        for (uint32_t i = 1; i < n; ++i) two |= g.row0[i] % T != 0;
-        if (two && !allow_two) {
-            uint32_t gb = 0;  // the tile height must divide every boundary
-            for (uint32_t i = 1; i < n; ++i) gb = std::gcd(gb, g.row0[i]);
-            uint32_t best = 0;
-            uint64_t best_rows = ~0ull;
-            for (uint32_t t = std::max(1u, T / 2); t <= 4 * T && t <= gb; ++t) {
-                if (gb % t) continue;
-                const uint64_t busiest = ((uint64_t)(sh.rows + t - 1) / t + cus - 1) / cus * t;
-                if (busiest < best_rows || (busiest == best_rows && t > best)) {
-                    best_rows = busiest;
-                    best = t;
-                }
-            }
-            if (best) {
-                T = best;
-                two = false;
-            }
-        }
-        grid = (sh.rows + T - 1) / T;
-        if (T <= min_rows && (allow_two || !two)) {
-            for (uint32_t P = 1; P <= sh.nb; ++P) {
-                if (sh.nb % P) continue;
-                if (P > 1 && M >= 4 && per_cu > 1) break;  // (phased kernels at M >= 4: one workgroup per CU)
-                const uint32_t K = sh.nb / P;
-                double best = 1e30;
-                uint32_t ps = 1;
-                for (uint32_t s = 1; s <= std::min<uint32_t>(K, W); ++s) {
-                    if (K % s) continue;
-                    const double rounds = std::ceil((double)T * s / W);
-                    const double cost = P * rounds * ((double)(K / s) + 0.25 * M);
-                    if (cost < best - 1e-9) {
-                        best = cost;
-                        ps = s;
-                    }
-                }
-                if (two && P > 1) break;  // (a tile spanning two tensors keeps every activation column resident)
-                const uint32_t xrow = K * 1024 + (mf ? 128 / M : 0);
-                const size_t head = 2 * (size_t)M * xrow + (((size_t)T * P * ps * M * 4 + 15) & ~(size_t)15);
-                const size_t lds = head + (two ? kTableBytes : 0);
-                if ((lds + fixed) * per_cu > 160 * 1024) continue;
-                sh.rows_per_wg = T;
-                sh.phases = P;
-                sh.phase_blocks = K;
-                sh.xrow = xrow;
-                sh.waves = W;
-                sh.psegs = ps;
-                sh.segs = P * ps;
-                sh.seg_blocks = K / ps;
-                sh.phase_units = T * ps;
-                const uint32_t pu = T * ps, rem = W % pu;
-                sh.dp = W / pu;
-                sh.dr = rem / ps;
-                sh.ds = rem - sh.dr * ps;
-                sh.tbl2_lds = two ? (uint32_t)head : 0u;
-                // the dispatcher gives each CU one of the first cu_count
-                // workgroups, then a second from the rest
-                sh.young_from = per_cu == 2 ? (uint32_t)cu_count() : ~0u;
-                grid_out = grid;
-                lds_out = lds;
-                two_out = two;
-                return true;
-            }
-        }
-        if (per_cu == 1) break;
-    }
-    return false;
-}
-
 typedef void (*SipKernel)(const SipGroup, const uint16_t*, const SipShape);
 
 // k_gemv_sip for M = 1, 2, 4, 8 (mi 0..3): one column phase (spanning tiles
@@ -2057,6 +1786,9 @@ SipKernel sip_kernel(int kind, int mi) {
     return table[kind][mi];
 }
 
+// One launch of the sip kernel over n tensors of equal cols (already
+// checked). Returns 2 when the group cannot run as one launch (a row tile
+// taller than a tensor, or tables past the LDS), having launched nothing.
 int launch_sip(const dmx_radix_tensor* const* ts, uint32_t n, const void* x, uint32_t m, const void* const* bias,
                int bias_dtype, void* const* out, int out_dtype, hipStream_t stream, char* err, size_t errn) {
     if (n < 1 || n > (uint32_t)kGroupMax || m < 1 || m > 8) return 2;
@@ -2094,7 +1826,8 @@ int launch_sip(const dmx_radix_tensor* const* ts, uint32_t n, const void* x, uin
     uint32_t grid = 0;
     size_t lds = 0;
     bool two = false;
-    if (!plan_launch(sh, g, n, min_rows, M, kSipWaves, kSipPerCu, sip_mfma((int)M), fixed, true, grid, lds, two))
+    if (!plan_launch(sh, g.row0, n, min_rows, M, kSipWaves, kSipPerCu, sip_mfma((int)M), false, fixed, true,
+                     (uint32_t)cu_count(), grid, lds, two))
         return 2;
     {
         const void* kerns[12];
@@ -2166,7 +1899,8 @@ int launch_gulp(const dmx_radix_tensor* const* ts, uint32_t n, const void* x, ui
     uint32_t grid = 0;
     size_t lds = 0;
     bool two = false;
-    if (!plan_launch(sh, g, n, min_rows, M, kSipWaves, kGulpPerCu, gulp_mfma((int)M), fixed, false, grid, lds, two))
+    if (!plan_launch(sh, g.row0, n, min_rows, M, kSipWaves, kGulpPerCu, gulp_mfma((int)M), false, fixed, false,
+                     (uint32_t)cu_count(), grid, lds, two))
         return 2;
     {
         const void* kerns[8];
@@ -2277,7 +2011,8 @@ int launch_decode_fast(const dmx_radix_tensor* t, uint16_t* out, hipStream_t str
     uint32_t grid = 0;
     size_t lds = 0;
     bool two = false;
-    if (!plan_launch(sh, g, 1, t->rows, 1, kSipWaves, kDecodePerCu, false, fixed, sip, grid, lds, two) ||
+    if (!plan_launch(sh, g.row0, 1, t->rows, 1, kSipWaves, kDecodePerCu, false, false, fixed, sip, (uint32_t)cu_count(),
+                     grid, lds, two) ||
         sh.phases > 1)
         return 2;
     const void* kern = sip ? reinterpret_cast<const void*>(k_gemv_sip<false, 1, false, kModeDecode>)
@@ -2436,8 +2171,9 @@ int launch_raw(const uint16_t* w, uint32_t rows, uint32_t cols, bool gulp, const
     uint32_t grid = 0;
     size_t lds = 0;
     bool two = false;
-    if (!plan_launch(sh, g, 1, rows, M, kSipWaves, gulp ? kGulpPerCu : kSipPerCu, gulp ? gulp_mfma((int)M) : sip_mfma((int)M),
-                     fixed, !gulp, grid, lds, two))
+    if (!plan_launch(sh, g.row0, 1, rows, M, kSipWaves, gulp ? kGulpPerCu : kSipPerCu,
+                     gulp ? gulp_mfma((int)M) : sip_mfma((int)M), false, fixed, !gulp, (uint32_t)cu_count(), grid, lds,
+                     two))
         return 2;
     if ((uint64_t)sh.rows_per_wg * cols * 2 >= (1ull << 31)) return 2;  // a tile's bytes within the buffer range
     {

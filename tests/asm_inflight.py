@@ -167,3 +167,19 @@ def kernels(asm: str, pattern: str):
         if re.search(pattern, m.group(1)):
             out[m.group(1)] = asm[m.end():asm.find(".Lfunc_end", m.end())]
     return out
+
+
+def metadata(asm: str) -> dict:
+    """-> {kernel name: {vgpr_count, sgpr_count, vgpr_spill_count,
+    sgpr_spill_count, private_segment_fixed_size}} from the code object's
+    metadata block of an assembly file."""
+    out = {}
+    for m in re.finditer(r"\.name:\s+(_Z\S+)\n(.*?)(?=\n\s+- \.|\n\.end_amdgpu_metadata)", asm, re.S):
+        fields = {}
+        for key in ("vgpr_count", "sgpr_count", "vgpr_spill_count", "sgpr_spill_count",
+                    "private_segment_fixed_size"):
+            mm = re.search(r"\." + key + r":\s+(\d+)", m.group(2))
+            if mm:
+                fields[key] = int(mm.group(1))
+        out[m.group(1)] = fields
+    return out

@@ -149,3 +149,24 @@ def test_every_sip_and_gulp_kernel_keeps_its_inflight_registers(kernel_asm):
         hazards, reached, total = analyse(body)
         assert reached == total, f"{name}: walked {reached} of {total} blocks"
         assert not hazards, f"{name}: {len(hazards)} in-flight register uses, first {hazards[0][2]!r}"
+
+
+def test_no_scratch_and_no_vgpr_spill_in_kernels_with_untracked_loads(kernel_asm):
+    """A VGPR spill, or any scratch access, between an untracked load and its
+    wait would move registers the compiler thinks are ready; SGPR spills go
+    to lanes of VGPRs (v_writelane / v_readlane), which the in-flight walk
+    above watches like any other register write or read. So: no scratch
+    instruction and no VGPR spill in any of these kernels; SGPR spills are
+    counted and reported."""
+    from tests.asm_inflight import metadata
+
+    ks = kernels(kernel_asm, r"k_gemv_(sip|gulp)I")
+    md = metadata(kernel_asm)
+    sgpr_spills = {}
+    for name, body in ks.items():
+        assert name in md, f"{name}: no metadata"
+        assert md[name].get("vgpr_spill_count", 0) == 0, f"{name}: {md[name]['vgpr_spill_count']} VGPR spills"
+        assert "scratch_" not in body, f"{name}: scratch access"
+        sgpr_spills[name] = md[name].get("sgpr_spill_count", 0)
+        assert body.count("v_writelane_b32") >= sgpr_spills[name] > 0 or sgpr_spills[name] == 0
+    print("SGPR spills (to VGPR lanes):", {k[20:60]: v for k, v in sgpr_spills.items() if v})
