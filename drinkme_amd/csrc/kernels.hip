@@ -469,6 +469,120 @@ __device__ __forceinline__ void mf_unit_end(f32x4 (&d)[M], float* out, uint32_t 
 }
 
 
+// Verify rows contracted four output rows at once (quad units). A wave
+// decodes the blocks of rows 4q .. 4q + 3 at one column block in turn, each
+// into its eight pair words h[j] (lane l: weights 16l .. 16l + 15 of row j),
+// then transposes the four rows over the lanes of each quad so that lane
+// 4b + i holds row i's weights 64b .. 64b + 63 (register set r: the 16
+// weights lane 4b + r decoded). v_mfma_f32_4x4x4_16b_bf16 contracts 16
+// independent 4 x 4 x 4 blocks; lane 4b + j of its result register i holds
+// the sum over k < 4 of A[4b + i][k] B[4b + j][k] (its lane layout checked
+// on gfx950 with integer operands). With A lane 4b + i = activation row i at
+// columns 64b + 4s .. 64b + 4s + 3 and B lane 4b + j = output row j at the
+// same columns, MFMA s (16 per block of four rows) keeps every product: lane
+// 4b + j accumulates activation row i (register i) times output row j over
+// its 64 columns, and a unit's end sums the 16 quads b.
+typedef short bf16x4_t __attribute__((ext_vector_type(4)));
+
+// The 4 x 4 transpose within each quad of lanes of four rows' pair words:
+// after it, h[r][w] of lane 4b + i is the word w that lane 4b + r held for
+// row i. Two butterfly stages, one per lane bit, each DPP reads of the
+// partner lane and one blend per word. A blend is a byte permute with a
+// per-lane selector (one v_perm_b32: the word a where the lane's bit is set,
+// else b); written as selects, the compiler turns them into selects of
+// array addresses, and the arrays into scratch.
+__device__ __forceinline__ uint32_t blend(uint32_t sel, uint32_t a, uint32_t b) { return __builtin_amdgcn_perm(a, b, sel); }
+
+__device__ __forceinline__ void quad_transpose(uint32_t (&h)[4][8], uint32_t lane) {
+    const uint32_t m0 = lane & 1u ? 0x07060504u : 0x03020100u, m1 = lane & 2u ? 0x07060504u : 0x03020100u;
+    // stage on lane bit 0 (partner lane ^ 1, quad_perm 1,0,3,2) against rows
+    // (0, 1) and (2, 3): the lane with bit 0 clear keeps row a and takes its
+    // partner's row a into row a + 1; the other keeps row a + 1 and takes its
+    // partner's row a + 1 into row a. (Every source lane of a quad_perm is
+    // valid, so the DPP moves have no old value to keep.)
+#pragma unroll
+    for (int w = 0; w < 8; ++w) {
+#pragma unroll
+        for (int a = 0; a < 4; a += 2) {
+            const uint32_t u0 = __builtin_amdgcn_mov_dpp(h[a][w], 0xB1, 0xF, 0xF, true);
+            const uint32_t u1 = __builtin_amdgcn_mov_dpp(h[a + 1][w], 0xB1, 0xF, 0xF, true);
+            h[a][w] = blend(m0, u1, h[a][w]);
+            h[a + 1][w] = blend(m0, h[a + 1][w], u0);
+        }
+    }
+    // the same on lane bit 1 (partner ^ 2, quad_perm 2,3,0,1), rows (0, 2), (1, 3)
+#pragma unroll
+    for (int w = 0; w < 8; ++w) {
+#pragma unroll
+        for (int a = 0; a < 2; ++a) {
+            const uint32_t u0 = __builtin_amdgcn_mov_dpp(h[a][w], 0x4E, 0xF, 0xF, true);
+            const uint32_t u2 = __builtin_amdgcn_mov_dpp(h[a + 2][w], 0x4E, 0xF, 0xF, true);
+            h[a][w] = blend(m1, u2, h[a][w]);
+            h[a + 2][w] = blend(m1, h[a + 2][w], u0);
+        }
+    }
+}
+
+// The eight pair words of a decoded block, required in registers here:
+// ordered before the next volatile statement (the refill of the stage the
+// block came from), so its decode is not deferred past that load and the
+// stage's old and new registers never overlap (which would take copies of
+// registers whose loads are still in flight).
+__device__ __forceinline__ void settle(const uint32_t (&h)[8]) {
+    asm volatile("" ::"v"(h[0]), "v"(h[1]), "v"(h[2]), "v"(h[3]), "v"(h[4]), "v"(h[5]), "v"(h[6]), "v"(h[7]));
+}
+
+// One quad step's products: the transposed rows h against the activation
+// rows at xq (the lane's A address in the step's column block: activation
+// row lane % 4, chunk 4 (lane / 4); chunk c of a 1024-column block holds
+// columns 16c .. 16c + 7, chunk 64 + c columns 16c + 8 .. 16c + 15), rows
+// 4g .. 4g + 3 of the activation into d[g] (even and odd MFMAs into
+// separate chains). x4 is four activation rows' LDS stride in bytes.
+template <int G>
+__device__ __forceinline__ void quad_mfma(f32x4 (&d)[G][2], const uint8_t* xq, uint32_t x4, const uint32_t (&h)[4][8]) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+            // MFMAs s = 4r + 2 half, + 1: columns 64b + 16r + 8 half .. + 7
+            const bf16x4_t b0 = __builtin_bit_cast(bf16x4_t, make_uint2(h[r][4 * half], h[r][4 * half + 1]));
+            const bf16x4_t b1 = __builtin_bit_cast(bf16x4_t, make_uint2(h[r][4 * half + 2], h[r][4 * half + 3]));
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                uint4 a;
+                __builtin_memcpy(&a, xq + g * x4 + 1024 * half + 16 * r, 16);
+                d[g][0] = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(__builtin_bit_cast(bf16x4_t, make_uint2(a.x, a.y)), b0,
+                                                               d[g][0], 0, 0, 0);
+                d[g][1] = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(__builtin_bit_cast(bf16x4_t, make_uint2(a.z, a.w)), b1,
+                                                               d[g][1], 0, 0, 0);
+            }
+        }
+    }
+}
+
+// A quad unit's sums: lane 4b + j's chains summed, then over the 16 quads b
+// (a fixed butterfly: every lane of a residue class gets the same bits);
+// lane j < 4 stores output row 4q + j's sums for activation rows 4g + i into
+// red[(slot0 + j S) M + 4g + i] where that row is in the tile. The chains are
+// cleared.
+template <int M, int G>
+__device__ __forceinline__ void quad_unit_end(f32x4 (&d)[G][2], float* red, uint32_t slot0, uint32_t segs,
+                                              uint32_t row0, uint32_t nrows, uint32_t lane) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        f32x4 s = d[g][0] + d[g][1];
+#pragma unroll
+        for (int k = 4; k < 64; k <<= 1)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) s[i] += __shfl_xor(s[i], k, kWave);
+        if (lane < 4 && row0 + lane < nrows) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) red[(slot0 + lane * segs) * M + 4 * g + i] = s[i];
+        }
+        d[g][0] = d[g][1] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+}
+
 // A group of sip tensors that share the activation (the q/k/v or gate/up
 // projections of a layer) runs as one launch: their rows form one row
 // space, tensor i's from row0[i]. The host keeps the row tile no taller than
@@ -587,6 +701,7 @@ __device__ __forceinline__ SipStage raw_load(i32x4 rsrc, uint32_t off, const Sip
 // unit.
 struct SipRef {
     uint32_t slot, cb, t, p;  // (decode mode: t is the block's index in its tensor, the output's block)
+    uint32_t row;             // quad mode: the quad's first row in the tile
     bool last;
 };
 
@@ -672,9 +787,12 @@ __device__ __forceinline__ void sip_table(uint2* tb, const uint32_t* palette) {
 constexpr int kModeGemv = 0, kModeTwinSip = 1, kModeTwinGulp = 2, kModeDecode = 3;
 
 template <bool TWO, int M, bool PH, int MODE = kModeGemv>
-__global__ __launch_bounds__(kSipThreads, (M == 8 || (PH && M == 4)) ? 3 : 6) void k_gemv_sip(const SipGroup g, const uint16_t* __restrict__ x,
-                                                          const SipShape sh) {
+__global__ __launch_bounds__(kSipThreads, (M == 8 || (M == 4 && (PH || (MODE != kModeTwinGulp && sip_quad(4))))) ? 3 : 6)
+void k_gemv_sip(const SipGroup g, const uint16_t* __restrict__ x, const SipShape sh) {
     constexpr bool RAW = MODE == kModeTwinSip || MODE == kModeTwinGulp, DEC = MODE == kModeDecode;
+    // verify rows four output rows at a time on the matrix cores (a raw twin
+    // mirroring gulp: gulp's rule)
+    constexpr bool QUAD = !DEC && (MODE == kModeTwinGulp ? gulp_quad(M) : sip_quad(M));
     static_assert(!(TWO && MODE), "the raw twin and the decode run one tensor");
     static_assert(!DEC || (M == 1 && !PH), "the decode runs unphased");
     // fixed-size tables in static LDS (their addresses fold into the LDS
@@ -698,7 +816,7 @@ __global__ __launch_bounds__(kSipThreads, (M == 8 || (PH && M == 4)) ? 3 : 6) vo
     const uint32_t nrows = wp0.nrows, ia = wp0.ia, ib = wp0.ib, row_a = wp0.row_a, row_b = wp0.row_b;
     const uint32_t split = wp0.split, lrow_a = wp0.lrow_a;
     const SipSpan sp = wp0.sp;
-    const uint32_t units = nrows * sh.segs;
+    const uint32_t units = (QUAD ? (nrows + 3) / 4 : nrows) * sh.segs;
     const bool two = TWO && split < nrows;
     const uint32_t* data_a = pick(g.data, ia);
     const uint32_t* data_b = pick(g.data, ib);
@@ -713,8 +831,12 @@ __global__ __launch_bounds__(kSipThreads, (M == 8 || (PH && M == 4)) ? 3 : 6) vo
     // the first two blocks' loads go out before the tables are built; a
     // cursor past the wave's work reads the workgroup's first block instead
     SipCursor p;
-    const SipWalk wk = sip_walk<false>(sh, nrows);
-    sip_start<TWO>(sh, p, wv, wk, sp);
+    QuadCursor pq;
+    const SipWalk wk = sip_walk<QUAD>(sh, nrows);
+    if constexpr (QUAD)
+        quad_start(sh, pq, wv, wk);
+    else
+        sip_start<TWO>(sh, p, wv, wk, sp);
     // each tensor's payload window: from the workgroup's first block of it
     // (the raw twin: from the workgroup's first row, 512 words a block)
     uint32_t base_a = 0, base_b = 0;
@@ -727,18 +849,34 @@ __global__ __launch_bounds__(kSipThreads, (M == 8 || (PH && M == 4)) ? 3 : 6) vo
     const SipLanes ln = sip_lanes(lane);
     SipRef nr;  // the last next_offsets() block
     auto next_offsets = [&]() {
-        const Issue is = sip_issue<TWO>(sh, p, sp);
-        nr.t = DEC ? p.blk : is.t;
-        nr.slot = p.slot;
-        nr.cb = p.cb;
-        nr.p = p.p;
-        nr.last = p.j + 1 == sh.seg_blocks;
+        Issue is;
+        if constexpr (QUAD) {
+            // (the four blocks of a quad step share its column block, phase
+            // and unit: row 4q's partial is slot, row 4q + j's slot + j S)
+            is = quad_issue<TWO>(sh, pq, sp, nrows);
+            nr.t = is.t;
+            nr.row = 4 * pq.q;
+            nr.slot = nr.row * sh.segs + pq.p * sh.psegs + pq.sp;
+            nr.cb = pq.sp * sh.seg_blocks + pq.c;
+            nr.p = pq.p;
+            nr.last = pq.c + 1 == sh.seg_blocks;
+        } else {
+            is = sip_issue<TWO>(sh, p, sp);
+            nr.t = DEC ? p.blk : is.t;
+            nr.slot = p.slot;
+            nr.cb = p.cb;
+            nr.p = p.p;
+            nr.last = p.j + 1 == sh.seg_blocks;
+        }
         uint2 o;
         if constexpr (RAW)  // the block's byte offset from the workgroup's first row
             o = make_uint2((is.blk - sp.a_first) * 2048u, 0u);
         else
             o = sip_offsets(TWO && is.t ? offsets_b : offsets_a, is.blk);
-        sip_next<TWO>(sh, p, wk, sp);
+        if constexpr (QUAD)
+            quad_next(sh, pq, wk);
+        else
+            sip_next<TWO>(sh, p, wk, sp);
         return o;
     };
     auto load = [&](uint2 o, uint32_t t) {
@@ -762,9 +900,16 @@ __global__ __launch_bounds__(kSipThreads, (M == 8 || (PH && M == 4)) ? 3 : 6) vo
     // two A/B runs; at M = 1 the same pipeline was 1.7% slower on the step
     // and 6% on 4096 x 4096; at M = 2, mixed)
     constexpr bool DEEP = M >= 4;
-    SipStage sC;
+    SipStage sC, sD;
+    SipRef rD;
     if constexpr (DEEP) {
         sC = load(oC, rC.t);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    if constexpr (QUAD) {  // (quad steps keep four blocks in flight: one step's)
+        const uint2 oD = next_offsets();
+        rD = nr;
+        sD = load(oD, rD.t);
         __builtin_amdgcn_sched_barrier(0);
     }
 
@@ -790,7 +935,11 @@ __global__ __launch_bounds__(kSipThreads, (M == 8 || (PH && M == 4)) ? 3 : 6) vo
     // they precede the two stages' 6 loads (raw: 4) in the wave's queue, so
     // vmcnt(6) completes them while the stages stay in flight
     if (threadIdx.x == 0) wg_done = 0;
-    if constexpr (RAW && DEEP)
+    if constexpr (RAW && QUAD)
+        asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+    else if constexpr (QUAD)
+        asm volatile("s_waitcnt vmcnt(12)" ::: "memory");
+    else if constexpr (RAW && DEEP)
         asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
     else if constexpr (RAW)
         asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
@@ -804,8 +953,8 @@ __global__ __launch_bounds__(kSipThreads, (M == 8 || (PH && M == 4)) ? 3 : 6) vo
     // M = 1 keeps two accumulator chains; M > 1 one per row
     float acc0 = 0.0f, acc1 = 0.0f;
     // verify rows on the matrix cores (a raw twin mirroring gulp: gulp's rule)
-    constexpr bool MF = MODE == kModeTwinGulp ? gulp_mfma(M) : sip_mfma(M);
-    constexpr int MA = MF ? 1 : M, MD = MF ? M : 1;
+    constexpr bool MF = !QUAD && (MODE == kModeTwinGulp ? gulp_mfma(M) : sip_mfma(M));
+    constexpr int MA = MF || QUAD ? 1 : M, MD = MF ? M : 1;
     float acc[MA];
 #pragma unroll
     for (int m = 0; m < MA; ++m) acc[m] = 0.0f;
@@ -813,6 +962,12 @@ __global__ __launch_bounds__(kSipThreads, (M == 8 || (PH && M == 4)) ? 3 : 6) vo
 #pragma unroll
     for (int m = 0; m < MD; ++m) dacc[m] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     const uint32_t mf_off = MF ? mf_lane_offset<MD>(lane, xrow) : 0u;
+    // quad mode: activation rows 4g .. 4g + 3 meet the four output rows in
+    // chains dq[g] (even and odd MFMAs)
+    constexpr int G = QUAD ? M / 4 : 1;
+    f32x4 dq[G][2];
+#pragma unroll
+    for (int g2 = 0; g2 < G; ++g2) dq[g2][0] = dq[g2][1] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     // one block of the wave's work, from its loaded stage
     // column phases: every wave walks all of them in order (so the barriers
     // match); a phase's activations replace the last one's once every wave
@@ -825,8 +980,10 @@ __global__ __launch_bounds__(kSipThreads, (M == 8 || (PH && M == 4)) ? 3 : 6) vo
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
     };
-    auto process = [&](const SipStage& s0, const SipRef& c) {
-        if (PH)
+    // (quad mode: the block's pair words go to hout, and the quad step does
+    // the products)
+    auto process = [&](const SipStage& s0, const SipRef& c, uint32_t* hout) {
+        if (PH && !QUAD)
             while (cur_phase < c.p) phase_advance();
         const uint16_t* xb;
         uint4 xa, xc;
@@ -940,6 +1097,18 @@ __global__ __launch_bounds__(kSipThreads, (M == 8 || (PH && M == 4)) ? 3 : 6) vo
             d[1] = make_uint4(wp[4], wp[5], wp[6], wp[7]);
             return;
         }
+        if constexpr (QUAD) {
+            if constexpr (RAW) {
+                // the raw twin's words are the stage's own registers, refilled
+                // next: copied out now, after the stage's wait
+#pragma unroll
+                for (int i = 0; i < 8; ++i) asm volatile("v_mov_b32 %0, %1" : "=v"(hout[i]) : "v"(wp[i]));
+            } else {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) hout[i] = wp[i];
+            }
+            return;
+        }
         if (M == 1) {
             acc0 = dot2(wp[0], xa.x, acc0);
             acc1 = dot2(wp[1], xa.y, acc1);
@@ -990,9 +1159,54 @@ __global__ __launch_bounds__(kSipThreads, (M == 8 || (PH && M == 4)) ? 3 : 6) vo
     // stage two blocks ahead, then completes the oldest (six loads newer);
     // whole rounds of three blocks, then the remainder
     const uint32_t my_units = wv < units ? (units - wv + kSipWaves - 1) / kSipWaves : 0;
-    const uint32_t items = my_units * sh.seg_blocks;
+    const uint32_t items = my_units * sh.seg_blocks * (QUAD ? 4 : 1);
     const uint32_t wg_items = units * sh.seg_blocks;
     const bool balance = !DEC && M <= 2 && wg_items >= kBalanceMinBlocks * kSipWaves;
+    if constexpr (QUAD) {
+        // a quad step: the four rows' blocks of one column block, stages A,
+        // B, C and D, each completed (nine loads newer: the other three
+        // stages; raw: six), decoded, and refilled at once with the block
+        // four ahead, the stage keeping its registers (no copies of a load
+        // in flight); then the four rows meet the activation rows on the
+        // matrix cores. A unit is whole steps: items is a multiple of four.
+        uint32_t hq[4][8];
+        const uint8_t* xq = reinterpret_cast<const uint8_t*>(xs) + (lane & 3u) * 2u * xrow + 64u * (lane >> 2);
+        for (uint32_t k = 0; k < items; k += 4) {
+            const SipRef step = rA;  // the step's column block, phase and unit (shared by its four blocks)
+            if constexpr (RAW) RAW_WAIT(6, sA); else SIP_WAIT(9, sA);
+            process(sA, rA, hq[0]);
+            settle(hq[0]);
+            uint2 oN = next_offsets();
+            rA = nr;
+            sA = load(oN, rA.t);
+            if constexpr (RAW) RAW_WAIT(6, sB); else SIP_WAIT(9, sB);
+            process(sB, rB, hq[1]);
+            settle(hq[1]);
+            oN = next_offsets();
+            rB = nr;
+            sB = load(oN, rB.t);
+            if constexpr (RAW) RAW_WAIT(6, sC); else SIP_WAIT(9, sC);
+            process(sC, rC, hq[2]);
+            settle(hq[2]);
+            oN = next_offsets();
+            rC = nr;
+            sC = load(oN, rC.t);
+            if constexpr (RAW) RAW_WAIT(6, sD); else SIP_WAIT(9, sD);
+            process(sD, rD, hq[3]);
+            settle(hq[3]);
+            oN = next_offsets();
+            rD = nr;
+            sD = load(oN, rD.t);
+            if (PH)
+                while (cur_phase < step.p) phase_advance();
+            quad_transpose(hq, lane);
+            quad_mfma<G>(dq, xq + step.cb * 2048u, 8u * xrow, hq);
+            if (step.last) quad_unit_end<M, G>(dq, red, step.slot, sh.segs, step.row, nrows, lane);
+        }
+        // in flight now: the four stages, past the wave's work; they land
+        // before the end
+        if constexpr (RAW) RAW_WAIT(0, sD); else SIP_WAIT(0, sD);
+    } else {
     uint32_t k = 0;
     for (; k + 3 <= items; k += 3) {
         if (balance) {
@@ -1018,17 +1232,17 @@ __global__ __launch_bounds__(kSipThreads, (M == 8 || (PH && M == 4)) ? 3 : 6) vo
             // three in flight: complete the oldest, then issue the block
             // three ahead in its place
             if constexpr (RAW) RAW_WAIT(4, sA); else SIP_WAIT(6, sA);
-            process(sA, rA);
+            process(sA, rA, nullptr);
             uint2 oN = next_offsets();
             rA = nr;
             sA = load(oN, rA.t);
             if constexpr (RAW) RAW_WAIT(4, sB); else SIP_WAIT(6, sB);
-            process(sB, rB);
+            process(sB, rB, nullptr);
             oN = next_offsets();
             rB = nr;
             sB = load(oN, rB.t);
             if constexpr (RAW) RAW_WAIT(4, sC); else SIP_WAIT(6, sC);
-            process(sC, rC);
+            process(sC, rC, nullptr);
             oN = next_offsets();
             rC = nr;
             sC = load(oN, rC.t);
@@ -1037,19 +1251,19 @@ __global__ __launch_bounds__(kSipThreads, (M == 8 || (PH && M == 4)) ? 3 : 6) vo
         uint2 oN = next_offsets();
         SipRef rN = nr;
         if constexpr (RAW) RAW_WAIT(4, sA); else SIP_WAIT(6, sA);
-        process(sA, rA);
+        process(sA, rA, nullptr);
         sA = load(oN, rN.t);
         rA = rN;
         oN = next_offsets();
         rN = nr;
         if constexpr (RAW) RAW_WAIT(4, sB); else SIP_WAIT(6, sB);
-        process(sB, rB);
+        process(sB, rB, nullptr);
         sB = load(oN, rN.t);
         rB = rN;
         oN = next_offsets();
         rN = nr;
         if constexpr (RAW) RAW_WAIT(4, sC); else SIP_WAIT(6, sC);
-        process(sC, rC);
+        process(sC, rC, nullptr);
         oC = oN;
         rC = rN;
         }
@@ -1057,16 +1271,17 @@ __global__ __launch_bounds__(kSipThreads, (M == 8 || (PH && M == 4)) ? 3 : 6) vo
     if constexpr (DEEP) {
         // in flight now: sA (older), sB, then sC (never a block of the wave's)
         if constexpr (RAW) RAW_WAIT(4, sA); else SIP_WAIT(6, sA);
-        if (k < items) process(sA, rA);
+        if (k < items) process(sA, rA, nullptr);
         if constexpr (RAW) RAW_WAIT(2, sB); else SIP_WAIT(3, sB);
-        if (k + 1 < items) process(sB, rB);
+        if (k + 1 < items) process(sB, rB, nullptr);
         if constexpr (RAW) RAW_WAIT(0, sC); else SIP_WAIT(0, sC);
     } else {
     // in flight now: sA (older), then sB
     if constexpr (RAW) RAW_WAIT(2, sA); else SIP_WAIT(3, sA);
-    if (k < items) process(sA, rA);
+    if (k < items) process(sA, rA, nullptr);
     if constexpr (RAW) RAW_WAIT(0, sB); else SIP_WAIT(0, sB);
-    if (k + 1 < items) process(sB, rB);
+    if (k + 1 < items) process(sB, rB, nullptr);
+    }
     }
     if constexpr (DEC) return;  // every load has landed (the waits above)
     if (PH)
@@ -1826,7 +2041,7 @@ int launch_sip(const dmx_radix_tensor* const* ts, uint32_t n, const void* x, uin
     uint32_t grid = 0;
     size_t lds = 0;
     bool two = false;
-    if (!plan_launch(sh, g.row0, n, min_rows, M, kSipWaves, kSipPerCu, sip_mfma((int)M), false, fixed, true,
+    if (!plan_launch(sh, g.row0, n, min_rows, M, kSipWaves, kSipPerCu, sip_mfma((int)M), sip_quad((int)M), fixed, true,
                      (uint32_t)cu_count(), grid, lds, two))
         return 2;
     {
@@ -1899,7 +2114,7 @@ int launch_gulp(const dmx_radix_tensor* const* ts, uint32_t n, const void* x, ui
     uint32_t grid = 0;
     size_t lds = 0;
     bool two = false;
-    if (!plan_launch(sh, g.row0, n, min_rows, M, kSipWaves, kGulpPerCu, gulp_mfma((int)M), false, fixed, false,
+    if (!plan_launch(sh, g.row0, n, min_rows, M, kSipWaves, kGulpPerCu, gulp_mfma((int)M), gulp_quad((int)M), fixed, false,
                      (uint32_t)cu_count(), grid, lds, two))
         return 2;
     {
@@ -2124,17 +2339,20 @@ extern "C" int dmx_gemv_narrow(const uint16_t* w, uint32_t rows, uint32_t cols, 
 typedef void (*RawKernel)(const SipGroup, const uint16_t*, const SipShape);
 
 // k_gemv_sip's raw instantiations: phased or not; M = 1, 2, 4, 8 (mi); at
-// M = 4 the matrix-core rule of the kernel mirrored (sip: MFMA, gulp:
-// v_dot2). At M = 1, 2 and 8 the sip and gulp kernels do the same
-// arithmetic, so one instantiation mirrors both.
-RawKernel raw_kernel(bool phased, int mi, bool gulp) {
-    static const RawKernel table[2][5] = {
+// M = 4 and 8 the verify-row rule of the kernel mirrored (sip: quad units on
+// the matrix cores; gulp: v_dot2 at M = 4, the one-row matrix-core path at
+// M = 8). At M = 1 and 2 the sip and gulp kernels do the same arithmetic,
+// so one instantiation mirrors both.
+constexpr int kRawKinds = 6;
+RawKernel raw_kernel(bool phased, int kind) {
+    static const RawKernel table[2][kRawKinds] = {
         {k_gemv_sip<false, 1, false, 1>, k_gemv_sip<false, 2, false, 1>, k_gemv_sip<false, 4, false, 1>,
-         k_gemv_sip<false, 8, false, 1>, k_gemv_sip<false, 4, false, 2>},
+         k_gemv_sip<false, 8, false, 1>, k_gemv_sip<false, 4, false, 2>, k_gemv_sip<false, 8, false, 2>},
         {k_gemv_sip<false, 1, true, 1>, k_gemv_sip<false, 2, true, 1>, k_gemv_sip<false, 4, true, 1>,
-         k_gemv_sip<false, 8, true, 1>, k_gemv_sip<false, 4, true, 2>}};
-    return table[phased ? 1 : 0][gulp && mi == 2 ? 4 : mi];
+         k_gemv_sip<false, 8, true, 1>, k_gemv_sip<false, 4, true, 2>, k_gemv_sip<false, 8, true, 2>}};
+    return table[phased ? 1 : 0][kind];
 }
+int raw_kind(int mi, bool gulp) { return gulp && mi >= 2 ? 2 + mi : mi; }
 
 // The twin over the fast kernels' work split: the plan the mirrored kernel
 // (sip, or gulp with `gulp`) makes for a tensor of this shape (its static
@@ -2172,19 +2390,20 @@ int launch_raw(const uint16_t* w, uint32_t rows, uint32_t cols, bool gulp, const
     size_t lds = 0;
     bool two = false;
     if (!plan_launch(sh, g.row0, 1, rows, M, kSipWaves, gulp ? kGulpPerCu : kSipPerCu,
-                     gulp ? gulp_mfma((int)M) : sip_mfma((int)M), false, fixed, !gulp, (uint32_t)cu_count(), grid, lds,
+                     gulp ? gulp_mfma((int)M) : sip_mfma((int)M), gulp ? gulp_quad((int)M) : sip_quad((int)M), fixed,
+                     !gulp, (uint32_t)cu_count(), grid, lds,
                      two))
         return 2;
     if ((uint64_t)sh.rows_per_wg * cols * 2 >= (1ull << 31)) return 2;  // a tile's bytes within the buffer range
     {
-        const void* kerns[10];  // (the raw kernels declare sip's static LDS)
+        const void* kerns[2 * kRawKinds];  // (the raw kernels declare sip's static LDS)
         for (int t = 0; t < 2; ++t)
-            for (int i = 0; i < 5; ++i) kerns[5 * t + i] = reinterpret_cast<const void*>(raw_kernel(t, i & 3, i == 4));
-        if (raise_lds_limit(kFamRaw, kerns, 10, lds, 64 * 1024 - kSipStaticLds, "raw twin kernel LDS opt-in", err,
+            for (int i = 0; i < kRawKinds; ++i) kerns[kRawKinds * t + i] = reinterpret_cast<const void*>(raw_kernel(t, i));
+        if (raise_lds_limit(kFamRaw, kerns, 2 * kRawKinds, lds, 64 * 1024 - kSipStaticLds, "raw twin kernel LDS opt-in", err,
                             errn))
             return 1;
     }
-    hipLaunchKernelGGL(raw_kernel(sh.phases > 1, mi, gulp), dim3(grid), dim3(kSipThreads), lds, stream, g,
+    hipLaunchKernelGGL(raw_kernel(sh.phases > 1, raw_kind(mi, gulp)), dim3(grid), dim3(kSipThreads), lds, stream, g,
                        static_cast<const uint16_t*>(x), sh);
     return launch_check(err, errn, "raw twin gemv launch");
 }

@@ -71,9 +71,10 @@ constexpr size_t kGulpStaticLds = kGulpT0Bytes + kTableBytes + 13 * 16 * 8 + 16 
 // latency, loses more from 5 waves than the products gain.
 DMX_HD constexpr bool sip_mfma(int M) { return M >= 4; }
 DMX_HD constexpr bool gulp_mfma(int M) { return M >= 8; }
-// Quad units (four output rows contracted at once on the matrix cores) for
-// the verify rows; off until the quad path is built.
-DMX_HD constexpr bool sip_quad(int M) { return false && M >= 4; }
+// Verify rows in quad units: four output rows contracted at once on the
+// matrix cores (sip at M = 4 and 8); the one-row matrix-core path stays
+// for gulp at M = 8.
+DMX_HD constexpr bool sip_quad(int M) { return M >= 4; }
 DMX_HD constexpr bool gulp_quad(int M) { return false && M >= 4; }
 
 struct SipShape {

@@ -13,8 +13,9 @@ loads that may still be in flight (loads retire in issue order;
 instruction that reads or writes one of their destination registers. The
 walk is path-sensitive in the 64-bit scalar constants (`s_mov_b64 X, -1|0`)
 that the compiler uses to steer `s_cbranch_vccnz`, and treats
-`s_cbranch_execz` as never taken where exec is known to be full (outside
-every `saveexec` region), so the branches of a wave-uniform if/else of two
+`s_cbranch_execz` as never taken and `s_cbranch_execnz` as always taken
+where exec is known to be full (outside every `saveexec` region: the
+kernels run whole waves), so the branches of a wave-uniform if/else of two
 load variants are not mixed.
 """
 
@@ -124,6 +125,8 @@ def analyse(text: str):
             return [idx[last.split()[1]]]
         if last.startswith("s_cbranch_execz") and exec_full:
             return nxt
+        if last.startswith("s_cbranch_execnz") and exec_full:
+            return [idx[last.split()[1]]]
         if last.startswith("s_cbranch_vccnz") and vcc is not None:
             return [idx[last.split()[1]]] if vcc else nxt
         if last.startswith("s_cbranch_vccz") and vcc is not None:
