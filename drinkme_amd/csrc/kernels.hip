@@ -382,92 +382,7 @@ __device__ __forceinline__ float row_sum16(float v) {
     return v;
 }
 
-// Verify rows (M = 4 or 8) on the matrix cores. v_mfma_f32_16x16x32_bf16
-// leaves in lane L, register v:
-//   D[L][v] += sum over g < 4, t < 8 of A[16 g + 4 (L / 16) + v][t] * B[16 g + L % 16][t]
-// where X[l][t] is element t of lane l's 8-element operand. B is the block's
-// decoded weights: half h of lane l is its weights 8h .. 8h + 7 (pair words
-// 4h .. 4h + 3). Variant s < M of A gives lane 16 g + i the M activation row
-// i / R at the columns of lane 16 g + R s + i % R's half-h weights
-// (R = 16 / M). So D_s, lane L, register v holds a dot product of matching
-// columns exactly where L % 16 == R s + (4 (L / 16) + v) % R: for M = 4 one
-// register per lane (s = (L % 16) / 4, v = L % 4, row L / 16); for M = 8 two
-// (s = (L % 16) / 2, v = L % 2 and 2 + L % 2, rows 2 (L / 16) and
-// 2 (L / 16) + 1). The other entries pair unrelated columns and are dropped.
-// Each lane's A operand is one 16-byte LDS read; the row stride of 2 K KB
-// plus 256 / M bytes puts the 16 lanes of a read on distinct banks.
-typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
-
-// The lane's A byte offset within an activation column block: row i / R,
-// the 16-byte chunk of column lane 16 g + i % R.
-template <int M>
-__device__ __forceinline__ uint32_t mf_lane_offset(uint32_t lane, uint32_t xrow) {
-    constexpr uint32_t R = 16 / M;
-    const uint32_t i = lane & 15u;
-    return (i / R) * (2u * xrow) + 16u * ((lane & ~15u) + i % R);
-}
-
-// One block into the M variants' accumulators: xa is the lane's A address
-// in the block's column block (chunk q of a 1024-column block holds columns
-// 16q .. 16q + 7 and chunk 64 + q columns 16q + 8 .. 16q + 15).
-template <int M>
-__device__ __forceinline__ void mf_block(f32x4 (&d)[M], const uint8_t* xa, const uint32_t (&wp)[8]) {
-    static_assert(M == 4 || M == 8, "matrix-core verify rows: M = 4 or 8");
-    constexpr uint32_t R = 16 / M;
-    const bf16x8_t b0 = __builtin_bit_cast(bf16x8_t, make_uint4(wp[0], wp[1], wp[2], wp[3]));
-    const bf16x8_t b1 = __builtin_bit_cast(bf16x8_t, make_uint4(wp[4], wp[5], wp[6], wp[7]));
-#pragma unroll
-    for (int s = 0; s < M; ++s) {
-        bf16x8_t a;
-        __builtin_memcpy(&a, xa + 16 * R * s, 16);
-        d[s] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b0, d[s], 0, 0, 0);
-    }
-#pragma unroll
-    for (int s = 0; s < M; ++s) {
-        bf16x8_t a;
-        __builtin_memcpy(&a, xa + 1024 + 16 * R * s, 16);
-        d[s] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b1, d[s], 0, 0, 0);
-    }
-}
-
-// A unit's M row sums from the accumulators (then cleared): each lane's
-// matching entries, summed over the 16 lanes of its row group, into
-// out[0 .. M).
-template <int M>
-__device__ __forceinline__ void mf_unit_end(f32x4 (&d)[M], float* out, uint32_t lane) {
-    static_assert(M == 4 || M == 8, "matrix-core verify rows: M = 4 or 8");
-    constexpr uint32_t R = 16 / M;
-    const uint32_t j = lane & 15u, s = j / R;
-    // d[s] by selects on the bits of s, over register copies: selects over
-    // the array itself would be folded into an indexed copy through scratch
-    f32x4 r[M];
-#pragma unroll
-    for (int k = 0; k < M; ++k) {
-        r[k] = d[k];
-        asm volatile("" : "+v"(r[k]));
-    }
-    const bool s0 = s & 1u, s1 = s & 2u;
-    f32x4 e = s1 ? (s0 ? r[3] : r[2]) : (s0 ? r[1] : r[0]);
-    if (M == 8) {
-        const f32x4 e2 = s1 ? (s0 ? r[M - 1] : r[M - 2]) : (s0 ? r[M - 3] : r[M - 4]);
-        e = (s & 4u) ? e2 : e;
-    }
-    const float lo = (j & 1u) ? e[1] : e[0], hi = (j & 1u) ? e[3] : e[2];
-    if (M == 4) {
-        const float v = row_sum16((j & 2u) ? hi : lo);
-        if (j == 15) out[lane >> 4] = v;
-    } else {
-        const float v0 = row_sum16(lo), v1 = row_sum16(hi);
-        if (j == 15) {
-            out[2 * (lane >> 4)] = v0;
-            out[2 * (lane >> 4) + 1] = v1;
-        }
-    }
-#pragma unroll
-    for (int k = 0; k < M; ++k) d[k] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-}
-
 
 // Verify rows contracted four output rows at once (quad units). A wave
 // decodes the blocks of rows 4q .. 4q + 3 at one column block in turn, each
@@ -787,7 +702,7 @@ __device__ __forceinline__ void sip_table(uint2* tb, const uint32_t* palette) {
 constexpr int kModeGemv = 0, kModeTwinSip = 1, kModeTwinGulp = 2, kModeDecode = 3;
 
 template <bool TWO, int M, bool PH, int MODE = kModeGemv>
-__global__ __launch_bounds__(kSipThreads, (M == 8 || (M == 4 && (PH || (MODE != kModeTwinGulp && sip_quad(4))))) ? 3 : 6)
+__global__ __launch_bounds__(kSipThreads, (M == 8 || (M == 4 && (PH || (MODE == kModeTwinGulp ? gulp_quad(4) : sip_quad(4))))) ? 3 : 6)
 void k_gemv_sip(const SipGroup g, const uint16_t* __restrict__ x, const SipShape sh) {
     constexpr bool RAW = MODE == kModeTwinSip || MODE == kModeTwinGulp, DEC = MODE == kModeDecode;
     // verify rows four output rows at a time on the matrix cores (a raw twin
@@ -953,15 +868,10 @@ void k_gemv_sip(const SipGroup g, const uint16_t* __restrict__ x, const SipShape
     // M = 1 keeps two accumulator chains; M > 1 one per row
     float acc0 = 0.0f, acc1 = 0.0f;
     // verify rows on the matrix cores (a raw twin mirroring gulp: gulp's rule)
-    constexpr bool MF = !QUAD && (MODE == kModeTwinGulp ? gulp_mfma(M) : sip_mfma(M));
-    constexpr int MA = MF || QUAD ? 1 : M, MD = MF ? M : 1;
+    constexpr int MA = QUAD ? 1 : M;  // v_dot2 rows (the quad path accumulates on the matrix cores)
     float acc[MA];
 #pragma unroll
     for (int m = 0; m < MA; ++m) acc[m] = 0.0f;
-    f32x4 dacc[MD];
-#pragma unroll
-    for (int m = 0; m < MD; ++m) dacc[m] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    const uint32_t mf_off = MF ? mf_lane_offset<MD>(lane, xrow) : 0u;
     // quad mode: activation rows 4g .. 4g + 3 meet the four output rows in
     // chains dq[g] (even and odd MFMAs)
     constexpr int G = QUAD ? M / 4 : 1;
@@ -1118,8 +1028,6 @@ void k_gemv_sip(const SipGroup g, const uint16_t* __restrict__ x, const SipShape
             acc1 = dot2(wp[5], xc.y, acc1);
             acc0 = dot2(wp[6], xc.z, acc0);
             acc1 = dot2(wp[7], xc.w, acc1);
-        } else if constexpr (MF) {
-            mf_block<MD>(dacc, reinterpret_cast<const uint8_t*>(xs) + mf_off + c.cb * 2048, wp);
         } else {
 #pragma unroll
             for (int m = 0; m < MA; ++m) {
@@ -1143,8 +1051,6 @@ void k_gemv_sip(const SipGroup g, const uint16_t* __restrict__ x, const SipShape
                 const float s = wave_sum_dpp(acc0 + acc1);
                 if (lane == 0) red[c.slot] = s;
                 acc0 = acc1 = 0.0f;
-            } else if constexpr (MF) {
-                mf_unit_end<MD>(dacc, red + c.slot * M, lane);
             } else {
 #pragma unroll
                 for (int m = 0; m < MA; ++m) {
@@ -1428,10 +1334,12 @@ __device__ __forceinline__ void gulp_tables(uint2* t0tab, uint2* t1tab, uint8_t*
 // DEC: decode only, each block's bf16 bits stored to the tensor's output
 // (row-major [rows, cols]) in place of the products.
 template <int M, bool PH, bool DEC = false>
-__global__ __launch_bounds__(kSipThreads, (M == 8 || (PH && M == 4)) ? 3 : 6) void k_gemv_gulp(const SipGroup g, const uint16_t* __restrict__ x,
-                                                                        const SipShape sh) {
+__global__ __launch_bounds__(kSipThreads, (M == 8 || (M == 4 && (PH || gulp_quad(4)))) ? 3 : 6)
+void k_gemv_gulp(const SipGroup g, const uint16_t* __restrict__ x, const SipShape sh) {
     static_assert(!DEC || (M == 1 && !PH), "the decode runs unphased");
     constexpr int W = kSipWaves, TH = kSipThreads;
+    // verify rows four output rows at a time on the matrix cores
+    constexpr bool QUAD = !DEC && gulp_quad(M);
     __shared__ uint2 t0tab[256];
     __shared__ uint2 t1tab[4096];
     __shared__ uint2 sel2[13 * 16];
@@ -1449,7 +1357,7 @@ __global__ __launch_bounds__(kSipThreads, (M == 8 || (PH && M == 4)) ? 3 : 6) vo
     const WgPlace wp0 = wg_place<false>(sh, g.row0, blockIdx.x);
     const uint32_t nrows = wp0.nrows, ia = wp0.ia, row_a = wp0.row_a, row_n = wp0.row_b, lrow = wp0.lrow_a;
     const SipSpan sp = wp0.sp;
-    const uint32_t units = nrows * sh.segs;
+    const uint32_t units = (QUAD ? (nrows + 3) / 4 : nrows) * sh.segs;
     const uint32_t* data = pick(g.data, ia);
     const uint32_t* offsets = pick(g.offsets, ia);
     const uint32_t* sched = reinterpret_cast<const uint32_t*>(pick(g.schedule, ia));
@@ -1458,19 +1366,30 @@ __global__ __launch_bounds__(kSipThreads, (M == 8 || (PH && M == 4)) ? 3 : 6) vo
     // the activation rows (first column phase), as in the sip kernel
     if constexpr (!DEC) load_x_slice<M, TH>(sh, x, xs, 0);
 
+    // p issues the loads, c follows it over the blocks processed (quad mode:
+    // pq and cq)
     SipCursor p, c;
-    const SipWalk wk = sip_walk<false>(sh, nrows);
-    sip_start<false>(sh, p, wv, wk, sp);
-    c = p;
+    QuadCursor pq, cq;
+    const SipWalk wk = sip_walk<QUAD>(sh, nrows);
+    if constexpr (QUAD) {
+        quad_start(sh, pq, wv, wk);
+        cq = pq;
+    } else {
+        sip_start<false>(sh, p, wv, wk, sp);
+        c = p;
+    }
     const uint32_t base = ((const_u32_ptr)offsets)[sp.a_first];
     const i32x4 rsrc = make_rsrc(data + base, 0x7FFFFFFFu);
     const GulpLanes ln = gulp_lanes(lane);
     uint32_t ns = 0;  // the schedule of the last next_offsets() block
     auto next_offsets = [&]() {
-        const uint32_t blk = sip_issue<false>(sh, p, sp).blk;
+        const uint32_t blk = QUAD ? quad_issue<false>(sh, pq, sp, nrows).blk : sip_issue<false>(sh, p, sp).blk;
         const uint2 o = sip_offsets(offsets, blk);
         ns = (((const_u32_ptr)sched)[blk >> 1] >> ((blk & 1u) * 16)) & 0xFFFFu;
-        sip_next<false>(sh, p, wk, sp);
+        if constexpr (QUAD)
+            quad_next(sh, pq, wk);
+        else
+            sip_next<false>(sh, p, wk, sp);
         return o;
     };
     const uint2 oA = next_offsets();
@@ -1483,7 +1402,14 @@ __global__ __launch_bounds__(kSipThreads, (M == 8 || (PH && M == 4)) ? 3 : 6) vo
     __builtin_amdgcn_sched_barrier(0);
     GulpStage sB = gulp_load(rsrc, base, oB, nB, ln);
     __builtin_amdgcn_sched_barrier(0);
-    GulpStage sC;
+    GulpStage sC, sD;
+    if constexpr (QUAD) {  // (quad steps keep four blocks in flight: one step's)
+        sC = gulp_load(rsrc, base, oC, nC, ln);
+        __builtin_amdgcn_sched_barrier(0);
+        const uint2 oD = next_offsets();
+        sD = gulp_load(rsrc, base, oD, ns, ln);
+        __builtin_amdgcn_sched_barrier(0);
+    }
 
     gulp_tables<TH>(t0tab, t1tab, reinterpret_cast<uint8_t*>(pal2w), pick(g.palette, ia));
     for (uint32_t i = threadIdx.x; i < 13 * 16; i += TH) {
@@ -1492,22 +1418,25 @@ __global__ __launch_bounds__(kSipThreads, (M == 8 || (PH && M == 4)) ? 3 : 6) vo
         for (uint32_t k = 0, r = o; k < 4; ++k) b[k] = (m >> k) & 1 ? (r++ & 7) : 0x0Cu;
         sel2[i] = make_uint2(b[0] | 0x0C00u | (b[1] << 16) | 0x0C000000u, b[2] | 0x0C00u | (b[3] << 16) | 0x0C000000u);
     }
-    // the activation's direct loads precede the two stages' 10 loads
-    asm volatile("s_waitcnt vmcnt(10)" ::: "memory");
+    // the activation's direct loads precede the stages' loads (two stages:
+    // 10; quad mode four: 20)
+    if constexpr (QUAD)
+        asm volatile("s_waitcnt vmcnt(20)" ::: "memory");
+    else
+        asm volatile("s_waitcnt vmcnt(10)" ::: "memory");
     __syncthreads();
 
     const uint32_t keep = 0x807F807Fu;
     const uint32_t* palg = pick(g.palette, ia);
     float acc0 = 0.0f, acc1 = 0.0f;
-    constexpr bool MF = gulp_mfma(M);  // verify rows on the matrix cores
-    constexpr int MA = MF ? 1 : M, MD = MF ? M : 1;
+    constexpr int MA = QUAD ? 1 : M;  // v_dot2 rows (the quad path accumulates on the matrix cores)
     float acc[MA];
 #pragma unroll
     for (int m = 0; m < MA; ++m) acc[m] = 0.0f;
-    f32x4 dacc[MD];
+    constexpr int G = QUAD ? M / 4 : 1;  // quad mode: activation rows 4g .. 4g + 3 in chains dq[g]
+    f32x4 dq[G][2];
 #pragma unroll
-    for (int m = 0; m < MD; ++m) dacc[m] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    const uint32_t mf_off = MF ? mf_lane_offset<MD>(lane, xrow) : 0u;
+    for (int g2 = 0; g2 < G; ++g2) dq[g2][0] = dq[g2][1] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
     // column phases: every wave walks all of them in order (so the barriers
     // match); a phase's activations replace the last one's once every wave
@@ -1520,8 +1449,10 @@ __global__ __launch_bounds__(kSipThreads, (M == 8 || (PH && M == 4)) ? 3 : 6) vo
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
     };
-    auto process = [&](const GulpStage& s0) {
-        if (PH)
+    // (quad mode: the block's pair words go to hout, and the quad step does
+    // the products)
+    auto process = [&](const GulpStage& s0, uint32_t* hout) {
+        if (PH && !QUAD)
             while (cur_phase < c.p) phase_advance();
         const uint32_t w1 = min(s0.sched & 0xFFu, kGulpT1Max), w2 = min(s0.sched >> 8, kGulpT2Max);
         const bool has_term = s0.end > s0.start + kGulpFixed + w1 + w2;
@@ -1686,6 +1617,12 @@ __global__ __launch_bounds__(kSipThreads, (M == 8 || (PH && M == 4)) ? 3 : 6) vo
             sip_next<false>(sh, c, wk, sp);
             return;
         }
+        if constexpr (QUAD) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) hout[i] = wp[i];
+            quad_next(sh, cq, wk);
+            return;
+        }
         if (M == 1) {
             acc0 = dot2(wp[0], xa.x, acc0);
             acc1 = dot2(wp[1], xa.y, acc1);
@@ -1695,8 +1632,6 @@ __global__ __launch_bounds__(kSipThreads, (M == 8 || (PH && M == 4)) ? 3 : 6) vo
             acc1 = dot2(wp[5], xc.y, acc1);
             acc0 = dot2(wp[6], xc.z, acc0);
             acc1 = dot2(wp[7], xc.w, acc1);
-        } else if constexpr (MF) {
-            mf_block<MD>(dacc, reinterpret_cast<const uint8_t*>(xs) + mf_off + c.cb * 2048, wp);
         } else {
 #pragma unroll
             for (int m = 0; m < MA; ++m) {
@@ -1719,8 +1654,6 @@ __global__ __launch_bounds__(kSipThreads, (M == 8 || (PH && M == 4)) ? 3 : 6) vo
                 const float s = wave_sum_dpp(acc0 + acc1);
                 if (lane == 0) red[c.slot] = s;
                 acc0 = acc1 = 0.0f;
-            } else if constexpr (MF) {
-                mf_unit_end<MD>(dacc, red + c.slot * M, lane);
             } else {
 #pragma unroll
                 for (int m = 0; m < MA; ++m) {
@@ -1733,7 +1666,51 @@ __global__ __launch_bounds__(kSipThreads, (M == 8 || (PH && M == 4)) ? 3 : 6) vo
         sip_next<false>(sh, c, wk, sp);
     };
     const uint32_t my_units = wv < units ? (units - wv + W - 1) / W : 0;
-    const uint32_t items = my_units * sh.seg_blocks;
+    const uint32_t items = my_units * sh.seg_blocks * (QUAD ? 4 : 1);
+    if constexpr (QUAD) {
+        // a quad step (as in the sip kernel): the four rows' blocks of one
+        // column block, stages A, B, C and D, each completed (15 loads newer:
+        // the other three stages), decoded and refilled at once with the
+        // block four ahead; then the four rows meet the activation rows on
+        // the matrix cores. One workgroup per CU (its registers), so no
+        // workgroup priorities.
+        uint32_t hq[4][8];
+        const uint8_t* xq = reinterpret_cast<const uint8_t*>(xs) + (lane & 3u) * 2u * xrow + 64u * (lane >> 2);
+        for (uint32_t k = 0; k < items; k += 4) {
+            // the step's column block, phase and unit (shared by its four blocks)
+            const uint32_t st_cb = cq.sp * sh.seg_blocks + cq.c, st_p = cq.p, st_row = 4 * cq.q;
+            const uint32_t st_slot = st_row * sh.segs + cq.p * sh.psegs + cq.sp;
+            const bool st_last = cq.c + 1 == sh.seg_blocks;
+            GULP_WAIT(15, sA);
+            process(sA, hq[0]);
+            settle(hq[0]);
+            uint2 oN = next_offsets();
+            sA = gulp_load(rsrc, base, oN, ns, ln);
+            GULP_WAIT(15, sB);
+            process(sB, hq[1]);
+            settle(hq[1]);
+            oN = next_offsets();
+            sB = gulp_load(rsrc, base, oN, ns, ln);
+            GULP_WAIT(15, sC);
+            process(sC, hq[2]);
+            settle(hq[2]);
+            oN = next_offsets();
+            sC = gulp_load(rsrc, base, oN, ns, ln);
+            GULP_WAIT(15, sD);
+            process(sD, hq[3]);
+            settle(hq[3]);
+            oN = next_offsets();
+            sD = gulp_load(rsrc, base, oN, ns, ln);
+            if (PH)
+                while (cur_phase < st_p) phase_advance();
+            quad_transpose(hq, lane);
+            quad_mfma<G>(dq, xq + st_cb * 2048u, 8u * xrow, hq);
+            if (st_last) quad_unit_end<M, G>(dq, red, st_slot, sh.segs, st_row, nrows, lane);
+        }
+        // in flight now: the four stages, past the wave's work; they land
+        // before the end
+        GULP_WAIT(0, sD);
+    } else {
     // Two workgroups share each SIMD, and its arbiter issues for the older
     // one's waves first: alone, the first workgroup finishes well before
     // the second, which then runs its last blocks without the other's
@@ -1755,22 +1732,23 @@ __global__ __launch_bounds__(kSipThreads, (M == 8 || (PH && M == 4)) ? 3 : 6) vo
         uint2 oN = next_offsets();
         uint32_t nN = ns;
         GULP_WAIT(10, sA);
-        process(sA);
+        process(sA, nullptr);
         sA = gulp_load(rsrc, base, oN, nN, ln);
         oN = next_offsets();
         nN = ns;
         GULP_WAIT(10, sB);
-        process(sB);
+        process(sB, nullptr);
         sB = gulp_load(rsrc, base, oN, nN, ln);
         oC = next_offsets();
         nC = ns;
         GULP_WAIT(10, sC);
-        process(sC);
+        process(sC, nullptr);
     }
     GULP_WAIT(5, sA);
-    if (k < items) process(sA);
+    if (k < items) process(sA, nullptr);
     GULP_WAIT(0, sB);
-    if (k + 1 < items) process(sB);
+    if (k + 1 < items) process(sB, nullptr);
+    }
     if constexpr (DEC) return;  // every load has landed (the waits above)
     if (PH)
         while (cur_phase + 1 < sh.phases) phase_advance();
@@ -2041,7 +2019,7 @@ int launch_sip(const dmx_radix_tensor* const* ts, uint32_t n, const void* x, uin
     uint32_t grid = 0;
     size_t lds = 0;
     bool two = false;
-    if (!plan_launch(sh, g.row0, n, min_rows, M, kSipWaves, kSipPerCu, sip_mfma((int)M), sip_quad((int)M), fixed, true,
+    if (!plan_launch(sh, g.row0, n, min_rows, M, kSipWaves, kSipPerCu, sip_quad((int)M), fixed, true,
                      (uint32_t)cu_count(), grid, lds, two))
         return 2;
     {
@@ -2114,7 +2092,7 @@ int launch_gulp(const dmx_radix_tensor* const* ts, uint32_t n, const void* x, ui
     uint32_t grid = 0;
     size_t lds = 0;
     bool two = false;
-    if (!plan_launch(sh, g.row0, n, min_rows, M, kSipWaves, kGulpPerCu, gulp_mfma((int)M), gulp_quad((int)M), fixed, false,
+    if (!plan_launch(sh, g.row0, n, min_rows, M, kSipWaves, gulp_per_cu((int)M), gulp_quad((int)M), fixed, false,
                      (uint32_t)cu_count(), grid, lds, two))
         return 2;
     {
@@ -2226,7 +2204,7 @@ int launch_decode_fast(const dmx_radix_tensor* t, uint16_t* out, hipStream_t str
     uint32_t grid = 0;
     size_t lds = 0;
     bool two = false;
-    if (!plan_launch(sh, g.row0, 1, t->rows, 1, kSipWaves, kDecodePerCu, false, false, fixed, sip, (uint32_t)cu_count(),
+    if (!plan_launch(sh, g.row0, 1, t->rows, 1, kSipWaves, kDecodePerCu, false, fixed, sip, (uint32_t)cu_count(),
                      grid, lds, two) ||
         sh.phases > 1)
         return 2;
@@ -2389,8 +2367,8 @@ int launch_raw(const uint16_t* w, uint32_t rows, uint32_t cols, bool gulp, const
     uint32_t grid = 0;
     size_t lds = 0;
     bool two = false;
-    if (!plan_launch(sh, g.row0, 1, rows, M, kSipWaves, gulp ? kGulpPerCu : kSipPerCu,
-                     gulp ? gulp_mfma((int)M) : sip_mfma((int)M), gulp ? gulp_quad((int)M) : sip_quad((int)M), fixed,
+    if (!plan_launch(sh, g.row0, 1, rows, M, kSipWaves, gulp ? gulp_per_cu((int)M) : kSipPerCu,
+                     gulp ? gulp_quad((int)M) : sip_quad((int)M), fixed,
                      !gulp, (uint32_t)cu_count(), grid, lds,
                      two))
         return 2;

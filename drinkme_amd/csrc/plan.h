@@ -65,17 +65,15 @@ constexpr uint32_t kGulpX2Words = 40;  // per wave: 128 exponent bytes + a windo
 constexpr size_t kSipStaticLds = kTableBytes + kSelBytes;
 constexpr size_t kGulpStaticLds = kGulpT0Bytes + kTableBytes + 13 * 16 * 8 + 16 + kPlanWaves * kGulpX2Words * 4;
 
-// Verify rows go to the matrix cores where that is faster: sip at M = 4 and
-// 8, gulp at M = 8. Gulp at M = 4 keeps v_dot2: its accumulators would take
-// it past the 80 registers of 6 waves per SIMD, and the decode, bound by
-// latency, loses more from 5 waves than the products gain.
-DMX_HD constexpr bool sip_mfma(int M) { return M >= 4; }
-DMX_HD constexpr bool gulp_mfma(int M) { return M >= 8; }
 // Verify rows in quad units: four output rows contracted at once on the
-// matrix cores (sip at M = 4 and 8); the one-row matrix-core path stays
-// for gulp at M = 8.
+// matrix cores, sip at M = 4 and 8, gulp at M = 8. The quad path holds four
+// decoded blocks in registers, so a gulp launch of it runs one workgroup
+// per CU; gulp's decode is bound by latency and wants the waves of two, so
+// at M = 4 it keeps v_dot2 (the quad path measured 4-13% slower there on
+// Qwen3-8B and 32B-class layers, and 4-8% faster at M = 8).
 DMX_HD constexpr bool sip_quad(int M) { return M >= 4; }
-DMX_HD constexpr bool gulp_quad(int M) { return false && M >= 4; }
+DMX_HD constexpr bool gulp_quad(int M) { return M >= 8; }
+DMX_HD constexpr uint32_t gulp_per_cu(int M) { return gulp_quad(M) ? 1u : kGulpPerCu; }
 
 struct SipShape {
     uint32_t rows, cols, nb;  // rows of the whole group
@@ -340,8 +338,8 @@ constexpr uint32_t kGulpT1Max = 64, kGulpT2Max = 128;  // the clamps of a schedu
 // column phases P (a divisor of NB) whose activation slice fits in LDS;
 // within a phase, the segments that give the fewest block-times per
 // workgroup (a unit's closing sum, one per activation row, costing about a
-// quarter of a block). W is the kernel's waves per workgroup, mf whether its
-// verify rows use the matrix cores, `fixed` its static LDS; a second
+// quarter of a block). W is the kernel's waves per workgroup, quad whether
+// its verify rows run in quad units, `fixed` its static LDS; a second
 // exponent table is added when a tile spans two tensors (allowed only with
 // `allow_two`). Without it, a group whose tensor boundaries the even tile
 // would cut takes the tile height, from T/2 to 4T, that divides every
@@ -349,8 +347,8 @@ constexpr uint32_t kGulpT1Max = 64, kGulpT2Max = 128;  // the clamps of a schedu
 // the resident ones run as a later round). Returns false, planning nothing,
 // when no plan fits.
 inline bool plan_launch(SipShape& sh, const uint32_t* row0, uint32_t n, uint32_t min_rows, uint32_t M, uint32_t W,
-                        uint32_t max_per_cu, bool mf, bool quad, size_t fixed, bool allow_two, uint32_t cus,
-                        uint32_t& grid_out, size_t& lds_out, bool& two_out) {
+                        uint32_t max_per_cu, bool quad, size_t fixed, bool allow_two, uint32_t cus, uint32_t& grid_out,
+                        size_t& lds_out, bool& two_out) {
     for (uint32_t per_cu = M == 8 ? 1 : max_per_cu; per_cu >= 1; --per_cu) {
         uint32_t grid = std::min<uint32_t>(sh.rows, cus * per_cu);
         uint32_t T = (sh.rows + grid - 1) / grid;
@@ -397,9 +395,8 @@ inline bool plan_launch(SipShape& sh, const uint32_t* row0, uint32_t n, uint32_t
                 if (two && P > 1) break;  // (a tile spanning two tensors keeps every activation column resident)
                 // the activation rows' stride: whole 1024-column blocks, plus
                 // 16 bytes for the quad path's 16-byte operand reads (four
-                // rows on distinct banks) or 256 / M bytes for the one-row
-                // matrix-core path's
-                const uint32_t xrow = K * 1024 + (quad ? 8 : mf ? 128 / M : 0);
+                // rows on distinct banks)
+                const uint32_t xrow = K * 1024 + (quad ? 8 : 0);
                 const size_t head = 2 * (size_t)M * xrow + (((size_t)T * P * ps * M * 4 + 15) & ~(size_t)15);
                 const size_t lds = head + (two ? kTableBytes : 0);
                 if ((lds + fixed) * per_cu > kLdsBytes) continue;

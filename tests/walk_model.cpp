@@ -64,7 +64,7 @@ std::string describe(const Case& c) {
 // The launch parameters each kernel's host code passes to plan_launch.
 struct Launch {
     uint32_t per_cu;
-    bool mf, quad, allow_two, gulp;
+    bool quad, allow_two, gulp;
     size_t fixed;
 };
 
@@ -72,8 +72,7 @@ Launch launch_of(Kind k, uint32_t M) {
     Launch l{};
     l.gulp = k == kGulp || k == kDecodeGulp || k == kTwinGulp;
     const bool dec = k == kDecodeSip || k == kDecodeGulp;
-    l.per_cu = dec ? kDecodePerCu : l.gulp ? kGulpPerCu : kSipPerCu;
-    l.mf = dec ? false : l.gulp ? gulp_mfma((int)M) : sip_mfma((int)M);
+    l.per_cu = dec ? kDecodePerCu : l.gulp ? gulp_per_cu((int)M) : kSipPerCu;
     l.quad = dec ? false : l.gulp ? gulp_quad((int)M) : sip_quad((int)M);
     l.allow_two = !l.gulp;
     l.fixed = l.gulp ? kGulpStaticLds : kSipStaticLds;
@@ -199,7 +198,7 @@ void run(const Case& cs) {
     uint32_t grid = 0;
     size_t lds = 0;
     bool two = false;
-    if (!plan_launch(sh, row0, n, min_rows, M, kPlanWaves, l.per_cu, l.mf, l.quad, l.fixed, l.allow_two, cs.cus, grid,
+    if (!plan_launch(sh, row0, n, min_rows, M, kPlanWaves, l.per_cu, l.quad, l.fixed, l.allow_two, cs.cus, grid,
                      lds, two))
         return;  // the generic kernel runs
     const bool dec = cs.kind == kDecodeSip || cs.kind == kDecodeGulp;
