@@ -572,18 +572,27 @@ __device__ __forceinline__ i32x4 make_rsrc(const void* base, uint32_t bytes) {
 // until at most N newer loads are outstanding completes the stage, whatever
 // other loads the compiler adds after it. Every read lies within the
 // block's start + 352 + 64 words, inside block_word_bounds(1024)[1] = 608.
-__device__ __forceinline__ SipStage sip_load(i32x4 rsrc, uint32_t base, uint2 o, uint32_t t, const SipLanes& ln) {
+// The terminal word goes through a resource spanning the block alone: a
+// lane past the block's last word reads 0 and fetches nothing (loading it
+// from the next block's literals, fetched again with that block, made the
+// traffic 7% above the block bytes; bitwise the same outputs, the Qwen3-8B
+// step 3.2% faster).
+__device__ __forceinline__ SipStage sip_load(i32x4 rsrc, uint32_t base, uint2 o, uint32_t t, const SipLanes& ln,
+                                             const uint32_t* data) {
     SipStage s;
     s.start = o.x;
     s.end = o.y;
     s.t = t;
     const uint32_t soff = (o.x - base) * 4u;
+    // the terminal through a resource of the block's own extent: a lane past
+    // the block's last word reads 0 and fetches nothing
+    const i32x4 rterm = make_rsrc(data + o.x, (o.y - o.x) * 4u);
     asm volatile(
-        "buffer_load_dword %0, %3, %6, %7 offen nt\n\t"
+        "buffer_load_dword %0, %3, %8, 0 offen nt\n\t"
         "buffer_load_dwordx2 %1, %4, %6, %7 offen nt\n\t"
         "buffer_load_dwordx4 %2, %5, %6, %7 offen nt"
         : "=&v"(s.term), "=&v"(s.t0), "=&v"(s.lit)
-        : "v"(ln.term), "v"(ln.t0), "v"(ln.lit), "s"(rsrc), "s"(soff));
+        : "v"(ln.term), "v"(ln.t0), "v"(ln.lit), "s"(rsrc), "s"(soff), "s"(rterm));
     return s;
 }
 
@@ -796,7 +805,7 @@ void k_gemv_sip(const SipGroup g, const uint16_t* __restrict__ x, const SipShape
     };
     auto load = [&](uint2 o, uint32_t t) {
         if constexpr (RAW) return raw_load(rsrc_a, o.x, ln);
-        return TWO && t ? sip_load(rsrc_b, base_b, o, 1u, ln) : sip_load(rsrc_a, base_a, o, 0u, ln);
+        return TWO && t ? sip_load(rsrc_b, base_b, o, 1u, ln, data_b) : sip_load(rsrc_a, base_a, o, 0u, ln, data_a);
     };
     const uint2 oA = next_offsets();
     SipRef rA = nr;
@@ -939,7 +948,7 @@ void k_gemv_sip(const SipGroup g, const uint16_t* __restrict__ x, const SipShape
         const uint2 sl0 = sel2[a0 >> 3], sl1 = sel2[(q1_ << 4) | (a1 >> 3)];
         const uint2 sl2 = sel2[(q2_ << 4) | (a2 >> 3)], sl3 = sel2[(q3_ << 4) | (a3 >> 3)];
         __builtin_amdgcn_sched_barrier(0);
-        const uint32_t q0 = wave_scan_incl(cnt) - cnt;
+        const uint32_t inc = wave_scan_incl(cnt), q0 = inc - cnt;
         // the terminal is read only when the directory gives the block words
         // past its fixed streams (radix_kernel_gpu.py:96-98); without it the
         // escaped exponents stay 0
@@ -968,8 +977,13 @@ void k_gemv_sip(const SipGroup g, const uint16_t* __restrict__ x, const SipShape
         // redoes its exponents with each group's four bytes read from the
         // terminal stream in memory (at most word 352 + 257 of the block:
         // inside the reach pad). Without a terminal the window was zero and
-        // every lane is already exact.
-        const bool wide = cnt > 8 || q0 > 243;
+        // every lane is already exact. So does every lane of a block whose
+        // terminal is shorter than its escapes (a malformed block the gate
+        // passes): its loaded words stop at the block's end, and the bytes
+        // past it are the following words, as a reader without an end bound
+        // takes them.
+        const bool short_term = has_term && __builtin_amdgcn_readlane(inc, 63) > 4u * (s0.end - s0.start - kSipFixed);
+        const bool wide = cnt > 8 || q0 > 243 || short_term;
         if (__builtin_expect(__builtin_amdgcn_ballot_w64(wide) != 0, 0) && has_term && wide) {
             E0 = tb[lo & 0xFFF];
             E1 = tb[(lo >> 12) & 0xFFF];
@@ -1248,33 +1262,43 @@ void k_gemv_sip(const SipGroup g, const uint16_t* __restrict__ x, const SipShape
 struct GulpStage {
     u32x4 lit;
     uint32_t t0, t1, t2, term;
-    uint32_t start, end, sched;
+    uint32_t lsched;  // the schedule entry | the block's length in words << 16
 };
 
+
+// A lane's buffer offset `off`, or, when it lies past byte `last`, that
+// offset with bit 31 set: past the 0x7FFFFFFF records of the workgroup's
+// buffer resource, so the lane reads 0 and fetches nothing (offsets here
+// stay far below 2^31, so the sign of last - off is the comparison).
+__device__ __forceinline__ uint32_t oob_past(uint32_t off, uint32_t last) {
+    return off | ((last - off) & 0x80000000u);
+}
 
 // The block's five loads through the workgroup's buffer resource (based at
 // its first block), untracked by the compiler as in sip_load; completed by
 // GULP_WAIT. Reads reach at most word 320 + 64 + 128 + 63 of the block,
-// inside block_word_bounds(1024)[1] = 768.
+// inside block_word_bounds(1024)[1] = 768. The terminal's 64 lanes reach far
+// past its few words: its lanes past the block's last word read 0 and fetch
+// nothing (else they load the next block's first words, which that block
+// fetches again).
 __device__ __forceinline__ GulpStage gulp_load(i32x4 rsrc, uint32_t base, uint2 o, uint32_t sched,
                                                const GulpLanes& ln) {
     GulpStage s;
-    s.start = o.x;
-    s.end = o.y;
-    s.sched = sched;
+    s.lsched = (sched & 0xFFFFu) | ((o.y - o.x) << 16);
     // (a schedule byte past its stream's widest keeps every read in the pad)
-    const uint32_t w1 = min(sched & 0xFFu, kGulpT1Max), w2 = min(sched >> 8, kGulpT2Max);
+    const uint32_t w1 = min(sched & 0xFFu, kGulpT1Max), w2 = min((sched >> 8) & 0xFFu, kGulpT2Max);
     const uint32_t soff = (o.x - base) * 4u;
     const uint32_t soff2 = soff + 4u * (kGulpFixed + w1);
-    const uint32_t soff3 = soff2 + 4u * w2;
+    // (the masked offset rides in its load's destination)
+    s.term = oob_past(ln.w + 4u * (kGulpFixed + w1 + w2), 4u * (o.y - o.x) - 1u);
     asm volatile(
-        "buffer_load_dword %0, %5, %8, %10 offen nt\n\t"
-        "buffer_load_dword %1, %6, %8, %9 offen nt\n\t"
-        "buffer_load_dword %2, %5, %8, %11 offen offset:1280 nt\n\t"
-        "buffer_load_dword %3, %5, %8, %11 offen offset:1024 nt\n\t"
-        "buffer_load_dwordx4 %4, %7, %8, %11 offen nt"
-        : "=&v"(s.term), "=&v"(s.t2), "=&v"(s.t1), "=&v"(s.t0), "=&v"(s.lit)
-        : "v"(ln.w), "v"(ln.t2), "v"(ln.lit), "s"(rsrc), "s"(soff2), "s"(soff3), "s"(soff));
+        "buffer_load_dword %0, %0, %5, %9 offen nt\n\t"
+        "buffer_load_dword %1, %6, %5, %8 offen nt\n\t"
+        "buffer_load_dword %2, %10, %5, %9 offen offset:1280 nt\n\t"
+        "buffer_load_dword %3, %10, %5, %9 offen offset:1024 nt\n\t"
+        "buffer_load_dwordx4 %4, %7, %5, %9 offen nt"
+        : "+&v"(s.term), "=&v"(s.t2), "=&v"(s.t1), "=&v"(s.t0), "=&v"(s.lit)
+        : "s"(rsrc), "v"(ln.t2), "v"(ln.lit), "s"(soff2), "s"(soff), "v"(ln.w));
     return s;
 }
 
@@ -1451,11 +1475,20 @@ void k_gemv_gulp(const SipGroup g, const uint16_t* __restrict__ x, const SipShap
     };
     // (quad mode: the block's pair words go to hout, and the quad step does
     // the products)
+    // the first word of the block being processed, from the directory at
+    // the block the cursor follows (only the rare paths need it, so no
+    // stage keeps it in a register)
+    auto block_start = [&]() {
+        // (row mode: c.blk rebuilt from the unit and column, which stay live)
+        const uint32_t blk = QUAD ? quad_issue<false>(sh, cq, sp, nrows).blk : row_block(sh, c, sp);
+        return ((const_u32_ptr)offsets)[blk];
+    };
     auto process = [&](const GulpStage& s0, uint32_t* hout) {
         if (PH && !QUAD)
             while (cur_phase < c.p) phase_advance();
-        const uint32_t w1 = min(s0.sched & 0xFFu, kGulpT1Max), w2 = min(s0.sched >> 8, kGulpT2Max);
-        const bool has_term = s0.end > s0.start + kGulpFixed + w1 + w2;
+        const uint32_t w1 = min(s0.lsched & 0xFFu, kGulpT1Max), w2 = min((s0.lsched >> 8) & 0xFFu, kGulpT2Max);
+        const uint32_t len = s0.lsched >> 16;
+        const bool has_term = len > kGulpFixed + w1 + w2;
         // tier 0
         const uint32_t T0 = s0.t0;
         uint2 E0 = t0tab[T0 & 0xFF];
@@ -1500,7 +1533,7 @@ void k_gemv_gulp(const SipGroup g, const uint16_t* __restrict__ x, const SipShap
         const uint32_t n2 = __builtin_amdgcn_readlane(inc1, 63);
         if (__builtin_expect(n2 > 128u || __builtin_amdgcn_ballot_w64(cnt2 > 8u) != 0, 0)) {
             // exact lane-serial path over the streams in memory
-            const uint32_t* tp = data + s0.start;
+            const uint32_t* tp = data + block_start();
             const uint32_t* s1 = tp + kGulpFixed;
             const uint32_t* s2 = s1 + w1;
             const uint32_t* s3 = s2 + w2;
@@ -1555,10 +1588,26 @@ void k_gemv_gulp(const SipGroup g, const uint16_t* __restrict__ x, const SipShap
             const bool ta = 2 * lane < n2 && ca == 15u, tb = 2 * lane + 1 < n2 && cb == 15u;
             if (__builtin_amdgcn_ballot_w64(ta || tb) != 0 && has_term) {
                 const uint32_t nt = (uint32_t)ta + (uint32_t)tb;
-                const uint32_t q3 = wave_scan_incl(nt) - nt;
+                const uint32_t inc3 = wave_scan_incl(nt), q3 = inc3 - nt;
                 // terminal byte r is byte r & 3 of word r >> 2, held by lane r >> 2
-                const uint32_t u0 = __builtin_amdgcn_ds_bpermute((int)((q3 >> 2) << 2), s0.term);
-                const uint32_t u1 = __builtin_amdgcn_ds_bpermute((int)(((q3 >> 2) + 1) << 2), s0.term);
+                const uint32_t a3 = (q3 >> 2) << 2;
+                uint32_t u0 = __builtin_amdgcn_ds_bpermute((int)a3, s0.term);
+                uint32_t u1 = __builtin_amdgcn_ds_bpermute((int)a3 + 4, s0.term);
+                const uint32_t tstart = kGulpFixed + w1 + w2;
+                if (__builtin_amdgcn_readlane(inc3, 63) > 4u * (len - tstart)) {
+                    // a terminal shorter than its escapes (a malformed block
+                    // the gate passes) loaded zeros past the block's end: its
+                    // words from memory, as a reader without an end bound
+                    // takes them (the wait also completes the stages in
+                    // flight)
+                    const uint32_t soff3 = (block_start() - base + tstart) * 4u;
+                    asm volatile("buffer_load_dword %0, %2, %3, %4 offen\n\t"
+                                 "buffer_load_dword %1, %2, %3, %4 offen offset:4\n\t"
+                                 "s_waitcnt vmcnt(0)"
+                                 : "=&v"(u0), "=&v"(u1)
+                                 : "v"(a3), "s"(rsrc), "s"(soff3)
+                                 : "memory");
+                }
                 const uint32_t tw = __builtin_amdgcn_alignbit(u1, u0, (q3 & 3u) << 3);
                 if (ta) ea = tw & 0xFFu;
                 if (tb) eb = ta ? (tw >> 8) & 0xFFu : tw & 0xFFu;

@@ -238,6 +238,13 @@ DMX_HD void sip_next(const SipShape& sh, SipCursor& c, const SipWalk& w, const S
     }
 }
 
+// A one-tensor row-mode cursor's block rebuilt from its unit and column
+// (c.blk while the cursor is on the wave's work), for code that keeps those
+// live but not c.blk.
+DMX_HD uint32_t row_block(const SipShape& sh, const SipCursor& c, const SipSpan& sp) {
+    return sp.a_first + c.r * sh.nb + c.p * sh.psegs * sh.seg_blocks + c.cb;
+}
+
 // The block a row-mode issue reads: the cursor's while it is on the wave's
 // work, else the workgroup's first block (of its first tensor).
 struct Issue {

@@ -8,9 +8,13 @@ and padded model (:149-182) are restated here for this build's kernels:
 
   - a directory whose blocks are cut short (a block that ends at its fixed
     streams, so the terminal is never read; a gulp block cut one word into
-    tier 1; and, below the descriptor gate, a whole block cut to 3 words
-    and a one-word tensor) decodes to oracle.padded_decode: every read past
-    the payload sees the pad's zeros;
+    tier 1; a block cut one word inside its terminal, whose last escapes
+    then read the next block's first word, or the pad; and, below the
+    descriptor gate, a whole block cut to 3 words and a one-word tensor)
+    decodes to oracle.padded_decode: every read past the payload sees the
+    pad's zeros, and every read past a block's end the words that follow
+    it, as drinkme's unmasked readers take them
+    (radix_kernel_gpu.py:313-316);
   - the allocation is payload | pad | 4096 sentinel words (0xFFFFFFFF, an
     exponent of 255 and a literal of 255 wherever one is read): no decoded
     bit and no GEMV sum may come from the sentinel; the gulp schedule the
@@ -65,6 +69,43 @@ def _fixed_words(p: O.Pack, block: int) -> int:
     return int(O.block_word_bounds(n, p.widths)[0])
 
 
+def _tiered_bits(rng, shape) -> np.ndarray:
+    """bf16 bits whose exponents fill the gulp tiers in order: 92% over six
+    (tiers 0 and 1), 6.5% over fifteen (tier 2), 1.5% over ten (the
+    terminal; sip's terminal holds these and most of the fifteen). A ragged
+    tail block gets a dozen terminal exponents."""
+    R, C = shape
+    u = rng.random((R, C))
+    main = rng.choice(np.arange(120, 126), size=(R, C), p=[.4, .25, .15, .1, .06, .04])
+    mid = rng.integers(105, 120, (R, C))
+    tail = rng.integers(126, 136, (R, C))
+    e = np.where(u < 0.92, main, np.where(u < 0.985, mid, tail))
+    if C % 1024:
+        e[-1, -12:] = tail[-1, -12:]
+    bits = (e.astype(np.uint16) << 7) | rng.integers(0, 128, (R, C), dtype=np.uint16)
+    return bits | (rng.integers(0, 2, (R, C), dtype=np.uint16) << 15)
+
+
+def _terminal_start(p: O.Pack, block: int) -> int:
+    """The word of block `block` its terminal stream starts at."""
+    t = _fixed_words(p, block)
+    if len(p.widths) > 2:
+        h = int(O.schedule(p)[block])
+        t += (h & 0xFF) + (h >> 8)
+    return t
+
+
+def _zeros_after(p: O.Pack, block: int, words: int) -> O.Pack:
+    """p with `words` zero words inserted after block `block`: its decode
+    of that block is a reader's that stops at the block's end."""
+    off = p.offsets.astype(np.int64)
+    end = int(off[block + 1])
+    data = np.concatenate([p.data[:end], np.zeros(words, np.uint32), p.data[end:]])
+    off[block + 1:] += words
+    off[block + 1] -= words  # (the block itself keeps its end)
+    return O.Pack(p.shape, p.block_size, p.widths, p.palette, off.astype(np.uint32), data)
+
+
 def _guarded(p: O.Pack, profile: str, cuda, zero_words: int, with_schedule: bool = True) -> dict:
     """A runtime dict over payload | zero_words zeros | SENTINEL_WORDS of
     0xFFFFFFFF, the gate not applied. The descriptor's pad is everything
@@ -102,6 +143,21 @@ def _cases(profile, C):
              "terminal-last": _cut_block(p, last, _fixed_words(p, last))}
     if profile == "gulp":
         cases["tier1-inner"] = _cut_block(p, 1, _fixed_words(p, 1) + 1)
+    # blocks cut one word inside their terminal: the escapes that lost their
+    # bytes read the following words (the next block's; the last block's
+    # are the pad's zeros). The tensor keeps the fast kernels' common path
+    # (gulp: under 128 tier-1 escapes a block) with terminals of several
+    # words. The inner case must discriminate: its decode differs from a
+    # reader's that stops at the block's end
+    pt = _pack(_tiered_bits(rng, (2, C)), profile)
+    for tag, b in (("inner", 1), ("last", last)):
+        ln = int(pt.offsets[b + 1]) - int(pt.offsets[b])
+        assert ln - 1 > _terminal_start(pt, b), f"block {b} has no terminal to cut"
+        q = _cut_block(pt, b, ln - 1)
+        if tag == "inner":
+            bounded = O.padded_decode(_zeros_after(q, b, 64))
+            assert not np.array_equal(O.padded_decode(q), bounded), "terminal-cut-inner does not discriminate"
+        cases[f"terminal-cut-{tag}"] = q
     for name, q in cases.items():
         O.validate(q)  # these pass the descriptor gate
     # below the gate: blocks cut inside their literal plane. Tight exponents

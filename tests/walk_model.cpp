@@ -149,6 +149,9 @@ void walk_launch(const Case& cs, const SipShape& sh, const uint32_t (&row0)[kGro
                     if (slot != r * sh.segs + cbg / L) bad(tag + ": wrong row partial");
                     if (cb != cbg % K || ph != cbg / K) bad(tag + ": wrong column block or phase");
                     if (last != (cbg % L == L - 1)) bad(tag + ": wrong unit end");
+                    // the gulp kernel's rare paths rebuild the block from the
+                    // unit and column
+                    if (!TWO && !sh.quad && row_block(sh, c, wp.sp) != is.blk) bad(tag + ": row_block != c.blk");
                     const size_t idx = (size_t)grow * sh.nb + cbg;
                     if (g_plant != 4 || idx != 0) ++seen[idx];
                     ++g_blocks;
