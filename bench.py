@@ -323,7 +323,8 @@ def main() -> int:
     dom_bytes = sum(gbytes[gi] for gi in dom) / len(dom)
     dom_us = dom_ms * 1e3 / len(dom)
     achieved = dom_bytes / (dom_us * 1e-6) / 1e9
-    log(f"dominant launch {dom_shape}: {dom_us:.2f} us/launch, {achieved:.0f} GB/s ({achieved / PEAK_GBPS:.1%} of peak)")
+    log(f"dominant launch {dom_shape}: {dom_us:.2f} us/launch, {achieved:.0f} GB/s ({achieved / PEAK_GBPS:.1%} of peak), "
+        f"{round(dom_bytes)} algorithmic bytes per launch")
     if args.kernel_only:
         # a plain copy of known size beside it: the scale for counter-derived bytes
         src = torch.empty(64 * 2**20, dtype=torch.float32, device="cuda").fill_(1.0)

@@ -1277,10 +1277,10 @@ __device__ __forceinline__ uint32_t oob_past(uint32_t off, uint32_t last) {
 // The block's five loads through the workgroup's buffer resource (based at
 // its first block), untracked by the compiler as in sip_load; completed by
 // GULP_WAIT. Reads reach at most word 320 + 64 + 128 + 63 of the block,
-// inside block_word_bounds(1024)[1] = 768. The terminal's 64 lanes reach far
-// past its few words: its lanes past the block's last word read 0 and fetch
-// nothing (else they load the next block's first words, which that block
-// fetches again).
+// inside block_word_bounds(1024)[1] = 768. Tier 1's and the terminal's 64
+// lanes reach far past their few words: their lanes past the block's last
+// word read 0 and fetch nothing (else they load the next block's first
+// words, which that block fetches again).
 __device__ __forceinline__ GulpStage gulp_load(i32x4 rsrc, uint32_t base, uint2 o, uint32_t sched,
                                                const GulpLanes& ln) {
     GulpStage s;
@@ -1289,15 +1289,17 @@ __device__ __forceinline__ GulpStage gulp_load(i32x4 rsrc, uint32_t base, uint2 
     const uint32_t w1 = min(sched & 0xFFu, kGulpT1Max), w2 = min((sched >> 8) & 0xFFu, kGulpT2Max);
     const uint32_t soff = (o.x - base) * 4u;
     const uint32_t soff2 = soff + 4u * (kGulpFixed + w1);
-    // (the masked offset rides in its load's destination)
-    s.term = oob_past(ln.w + 4u * (kGulpFixed + w1 + w2), 4u * (o.y - o.x) - 1u);
+    // (the masked offsets ride in their loads' destinations)
+    const uint32_t last = 4u * (o.y - o.x) - 1u;
+    s.term = oob_past(ln.w + 4u * (kGulpFixed + w1 + w2), last);
+    s.t1 = oob_past(ln.w, last - 4u * kGulpFixed);  // (read at offset:1280, word 320)
     asm volatile(
         "buffer_load_dword %0, %0, %5, %9 offen nt\n\t"
         "buffer_load_dword %1, %6, %5, %8 offen nt\n\t"
-        "buffer_load_dword %2, %10, %5, %9 offen offset:1280 nt\n\t"
+        "buffer_load_dword %2, %2, %5, %9 offen offset:1280 nt\n\t"
         "buffer_load_dword %3, %10, %5, %9 offen offset:1024 nt\n\t"
         "buffer_load_dwordx4 %4, %7, %5, %9 offen nt"
-        : "+&v"(s.term), "=&v"(s.t2), "=&v"(s.t1), "=&v"(s.t0), "=&v"(s.lit)
+        : "+&v"(s.term), "=&v"(s.t2), "+&v"(s.t1), "=&v"(s.t0), "=&v"(s.lit)
         : "s"(rsrc), "v"(ln.t2), "v"(ln.lit), "s"(soff2), "s"(soff), "v"(ln.w));
     return s;
 }
@@ -1511,8 +1513,21 @@ void k_gemv_gulp(const SipGroup g, const uint16_t* __restrict__ x, const SipShap
         const uint32_t q0 = wave_scan_incl_dpp(cnt1) - cnt1;
         // tier 1: the lane's codes, 2 bits each from bit 2 q0 of the stream
         const int k1 = (int)((q0 >> 2) & ~3u);
-        const uint32_t v0 = __builtin_amdgcn_ds_bpermute(k1, s0.t1);
-        const uint32_t v1 = __builtin_amdgcn_ds_bpermute(k1 + 4, s0.t1);
+        uint32_t v0 = __builtin_amdgcn_ds_bpermute(k1, s0.t1);
+        uint32_t v1 = __builtin_amdgcn_ds_bpermute(k1 + 4, s0.t1);
+        if (kGulpFixed + (__builtin_amdgcn_readlane(q0 + cnt1, 63) + 15u) / 16u > len) {
+            // a tier-1 stream past the block's end (a malformed block the
+            // gate passes) loaded zeros there: its words from memory, as a
+            // reader without an end bound takes them (the wait also
+            // completes the stages in flight)
+            const uint32_t soff1 = (block_start() - base) * 4u + 4u * kGulpFixed;
+            asm volatile("buffer_load_dword %0, %2, %3, %4 offen\n\t"
+                         "buffer_load_dword %1, %2, %3, %4 offen offset:4\n\t"
+                         "s_waitcnt vmcnt(0)"
+                         : "=&v"(v0), "=&v"(v1)
+                         : "v"(k1), "s"(rsrc), "s"(soff1)
+                         : "memory");
+        }
         const uint32_t W1 = __builtin_amdgcn_alignbit(v1, v0, (q0 & 15u) << 1);
 #define DMX_T1(E, off) t1tab[(__builtin_amdgcn_ubfe(W1, (off), 8) << 4) | ((E.x >> 3) & 15u)]
         const uint2 P0 = DMX_T1(E0, 0u), P1 = DMX_T1(E1, o1), P2 = DMX_T1(E2, o2), P3 = DMX_T1(E3, o3);

@@ -158,6 +158,13 @@ def _cases(profile, C):
             bounded = O.padded_decode(_zeros_after(q, b, 64))
             assert not np.array_equal(O.padded_decode(q), bounded), "terminal-cut-inner does not discriminate"
         cases[f"terminal-cut-{tag}"] = q
+    if profile == "gulp":
+        # the same tensor's block cut one word into tier 1 (on the fast
+        # kernel's common path, unlike tier1-inner's spread tensor)
+        q = _cut_block(pt, 1, _fixed_words(pt, 1) + 1)
+        assert not np.array_equal(O.padded_decode(q), O.padded_decode(_zeros_after(q, 1, 64))), \
+            "tier1-cut-inner does not discriminate"
+        cases["tier1-cut-inner"] = q
     for name, q in cases.items():
         O.validate(q)  # these pass the descriptor gate
     # below the gate: blocks cut inside their literal plane. Tight exponents
