@@ -30,7 +30,8 @@ Reported:
   roofline    the dominant kernel launch (the grouped gate/up GEMV of a
               layer, 2 x 12288 x 4096): its algorithmic bytes per launch /
               its average launch time, from HIP events around a graph of
-              its launches
+              its launches, timed after 0.3 s of untimed replays (the
+              first thing timed: the clocks settle first)
   cpu_baseline  drinkme's CPU route on the host's cores: the compiled
               drinkme decoder (oracle/_ref) + torch F.linear, on a bounded
               sample (layer 0), scaled to the step by weight count; three
@@ -103,8 +104,11 @@ def build_tensors(items, profile: str, m: int = 1):
     return tensors
 
 
-def time_graph(fn, replays: int, warmup: int) -> float:
-    """Milliseconds per replay of `fn` captured as a HIP graph."""
+def time_graph(fn, replays: int, warmup: int, settle_s: float = 0.0, info: dict | None = None) -> float:
+    """Milliseconds per replay of `fn` captured as a HIP graph. settle_s:
+    untimed replays for at least that long before the warmup ones (the GPU
+    comes out of the host-side packing at low clocks: a graph timed first,
+    over a few ms, reads up to 12% slow); their count goes to info."""
     import torch
 
     fn()
@@ -112,6 +116,14 @@ def time_graph(fn, replays: int, warmup: int) -> float:
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
         fn()
+    settle, t0 = 0, time.time()
+    while time.time() - t0 < settle_s:
+        for _ in range(10):
+            g.replay()
+        settle += 10
+        torch.cuda.synchronize()
+    if info is not None:
+        info["settle_replays"] = settle
     for _ in range(warmup):
         g.replay()
     torch.cuda.synchronize()
@@ -319,7 +331,8 @@ def main() -> int:
 
     total_bytes = sum(t["bytes"] for t in tensors)
     total_bf16 = sum(t["bf16_bytes"] for t in tensors)
-    dom_ms = time_graph(dominant, max(args.steps, 10), args.warmup)
+    dom_info = {}
+    dom_ms = time_graph(dominant, max(args.steps, 10), args.warmup, settle_s=0.3, info=dom_info)
     dom_bytes = sum(gbytes[gi] for gi in dom) / len(dom)
     dom_us = dom_ms * 1e3 / len(dom)
     achieved = dom_bytes / (dom_us * 1e-6) / 1e9
@@ -386,7 +399,7 @@ def main() -> int:
             "kernel": {"sip": "k_gemv_sip", "gulp": "k_gemv_gulp"}.get(args.profile, "k_gemv_generic"),
             "shape": dom_shape,
             "bytes_per_launch": round(dom_bytes), "us_per_launch": round(dom_us, 3),
-            "launches_timed": len(dom),
+            "launches_timed": len(dom), "settle_replays": dom_info["settle_replays"],
         },
         "cpu_baseline": cpu,
     }
