@@ -2,9 +2,11 @@
 grouped launch path the benchmark times (dmx_radix_gemv_group: q/k/v and
 gate/up of a layer as one launch each, o and down alone).
 
+  - the single 4096 x 4096 linear, N(0, 0.02), sip, M = 1;
   - Qwen3-8B layer (4096 hidden; q 4096x4096, k/v 1024x4096, o 4096x4096,
     gate/up 12288x4096, down 4096x12288), N(0, 0.02), sip, M = 1;
-  - the same layer at gulp, M = 4 (the MTP verify rows);
+  - the same layer at gulp, M = 4 (the MTP verify rows), and at sip, M = 4
+    (its blocks contracted on the matrix cores);
   - the Qwen3-8B lm_head, 151936 x 4096 N(0, 0.02), sip, M = 1: the largest
     launch of the decode-step sweep, with its own plan (about 2,400 blocks
     per CU, progress balance on);
@@ -110,6 +112,18 @@ def _layer(cuda, workload, copy, shapes, dist, profile, m, x_workload):
         torch.cuda.empty_cache()
 
 
+def test_linear_4096_sip_m1(cuda):
+    """The single-linear workload's first copy, the bench's own tensor."""
+    from drinkme_amd import synth
+
+    t0 = time.time()
+    print("case linear 4096x4096 sip M=1", flush=True)
+    bits = synth.weight("linear-4096", 0, "w", 4096, 4096)
+    rt = _resident(bits, "sip", cuda)
+    xb = synth.activation("linear-4096", "x4096", 1, 4096)
+    _check_group(cuda, t0, "linear-4096 sip M=1", [("w", bits, rt)], xb)
+
+
 def test_qwen3_8b_layer_sip_m1(cuda):
     from drinkme_amd import synth
 
@@ -120,6 +134,12 @@ def test_qwen3_8b_layer_gulp_m4(cuda):
     from drinkme_amd import synth
 
     _layer(cuda, "qwen3-8b", 0, synth.QWEN3_8B_LAYER, synth.NORMAL, "gulp", 4, "qwen3-8b-layer")
+
+
+def test_qwen3_8b_layer_sip_m4(cuda):
+    from drinkme_amd import synth
+
+    _layer(cuda, "qwen3-8b", 0, synth.QWEN3_8B_LAYER, synth.NORMAL, "sip", 4, "qwen3-8b-layer")
 
 
 def test_qwen3_8b_lm_head_sip_m1(cuda):
