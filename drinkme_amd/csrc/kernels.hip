@@ -2010,14 +2010,19 @@ int launch_check(char* err, size_t errn, const char* what) {
 
 bool is_sip(const dmx_radix_tensor* t) { return t->n_widths == 2 && t->widths[0] == 3 && t->widths[1] == 8; }
 
+// The current device's CU count, cached per device (the plans deal rows
+// to it).
 int cu_count() {
-    static std::atomic<int> cached{0};
-    int n = cached.load();
-    if (n) return n;
+    static std::mutex mu;
+    static std::map<int, int> cached;
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return 256;
+    std::lock_guard<std::mutex> lock(mu);
+    auto it = cached.find(dev);
+    if (it != cached.end()) return it->second;
+    int n = 0;
     if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-    cached.store(n);
+    cached.emplace(dev, n);
     return n;
 }
 
