@@ -106,7 +106,9 @@ def _run(blocks, k, consts, loads, issues):
                     if r in pend:
                         issues.append((blocks[k][0], n, ln, pend[r]))
         if op.startswith(_VMEM):
-            is_load = "load" in op and "lds" not in op
+            # (a load to LDS, as global_load_lds_* or a buffer load with the
+            # lds modifier, writes no VGPR: its first operand is its address)
+            is_load = "load" in op and "lds" not in op and not re.search(r"\slds\b", ln)
             loads = {x: (min(c + 1, _CAP), ds) for x, (c, ds) in loads.items()}
             loads[(k, n)] = (0, frozenset(_vregs(toks[0])) if (is_load and toks) else frozenset())
     return consts, loads, vcc

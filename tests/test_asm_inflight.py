@@ -60,6 +60,26 @@ def test_partial_wait_retires_only_the_older_loads():
     assert len(hz) == 1 and "v8, v4, v4" in hz[0][2]
 
 
+def test_a_load_to_lds_holds_no_register_but_counts_in_vmcnt():
+    # a buffer load with the lds modifier writes LDS, not its first operand
+    # (its address): reusing that register is fine. It still counts in
+    # vmcnt: vmcnt(1) after it retires the older load, so v1 is ready (were
+    # it not counted, v1's load would be the one left in flight)
+    body = """
+    buffer_load_dword v1, v10, s[0:3], s4 offen
+    buffer_load_dword v2, s[0:3], 0 offen lds
+    v_mov_b32_e32 v2, 0
+    s_waitcnt vmcnt(1)
+    v_add_u32_e32 v3, v1, v1
+    s_waitcnt vmcnt(0)
+    s_endpgm
+    """
+    assert _flagged(body) == []
+    # without the vmcnt(1), the read of v1 is flagged (and only it)
+    hz = _flagged(body.replace("s_waitcnt vmcnt(1)", ""))
+    assert len(hz) == 1 and "v3, v1, v1" in hz[0][2]
+
+
 def test_spill_and_reuse_of_an_inflight_register_are_flagged():
     body = """
     buffer_load_dword v1, v12, s[28:31], s18 offen
