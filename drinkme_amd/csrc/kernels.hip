@@ -8,9 +8,22 @@
 //   k_gemv_generic    decode + GEMV for any widths, block size, ragged rows,
 //                     M = 1..8 (radix_ops.gemv_fused / gemv_mc,
 //                     radix_kernel_gpu.py:682-718, radix_ops.py:91-164)
-//   k_gemv_sip        the M = 1 fused decode + GEMV for sip (3, 8) streams
-//                     over whole 1024-weight blocks and a bf16 activation —
-//                     the serial decode step's hot kernel
+//   k_gemv_sip        the fused decode + GEMV for sip (3, 8) streams over
+//                     whole 1024-weight blocks and M = 1..8 bf16 activation
+//                     rows (radix_kernel_gpu.py:682-718, radix_ops.py:91-164)
+//                     — the serial decode step's hot kernel; M = 4 and 8 in
+//                     quad units on the matrix cores. Its other modes: the
+//                     raw twin (a raw bf16 weight through the same plan and
+//                     sums, radix_kernel_gpu.py:639-668) and the decode
+//                     (each block's bits stored instead of the products)
+//   k_gemv_gulp       the same for gulp (2, 2, 4, 8) streams (the schedule's
+//                     stream lengths, radix_kernel_gpu.py:292-392); M = 8 in
+//                     quad units; a decode mode
+//   k_gemv_narrow     a raw row-major bf16 weight against M <= 8 rows
+//                     (radix_ops.gemv_narrow, radix_ops.py:177-249)
+//
+// The launch plan and the cursors that walk it are plan.h, shared with a
+// host model of the kernels' reads.
 //
 // Bit layout (src/drinkme/codec/radix.py:77-136): per block of n weights,
 // the 8-bit literal plane (sign << 7 | mantissa), then per nonterminal tier
@@ -2387,7 +2400,7 @@ typedef void (*RawKernel)(const SipGroup, const uint16_t*, const SipShape);
 
 // k_gemv_sip's raw instantiations: phased or not; M = 1, 2, 4, 8 (mi); at
 // M = 4 and 8 the verify-row rule of the kernel mirrored (sip: quad units on
-// the matrix cores; gulp: v_dot2 at M = 4, the one-row matrix-core path at
+// the matrix cores; gulp: v_dot2 at M = 4, quad units with gulp's tiles at
 // M = 8). At M = 1 and 2 the sip and gulp kernels do the same arithmetic,
 // so one instantiation mirrors both.
 constexpr int kRawKinds = 6;
