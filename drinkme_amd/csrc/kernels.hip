@@ -774,16 +774,6 @@ void k_gemv_sip(const SipGroup g, const uint16_t* __restrict__ x, const SipShape
         quad_start(sh, pq, wv, wk);
     else
         sip_start<TWO>(sh, p, wv, wk, sp);
-    // each tensor's payload window: from the workgroup's first block of it
-    // (the raw twin: from the workgroup's first row, 512 words a block)
-    uint32_t base_a = 0, base_b = 0;
-    if constexpr (!RAW) {
-        base_a = ((const_u32_ptr)offsets_a)[sp.a_first];
-        base_b = ((const_u32_ptr)offsets_b)[0];
-    }
-    const i32x4 rsrc_a = make_rsrc(RAW ? data_a + (uint64_t)sp.a_first * 512u : data_a + base_a, 0x7FFFFFFFu);
-    const i32x4 rsrc_b = make_rsrc(data_b + base_b, 0x7FFFFFFFu);
-    const SipLanes ln = sip_lanes(lane);
     SipRef nr;  // the last next_offsets() block
     auto next_offsets = [&]() {
         Issue is;
@@ -816,16 +806,34 @@ void k_gemv_sip(const SipGroup g, const uint16_t* __restrict__ x, const SipShape
             sip_next<TWO>(sh, p, wk, sp);
         return o;
     };
-    auto load = [&](uint2 o, uint32_t t) {
-        if constexpr (RAW) return raw_load(rsrc_a, o.x, ln);
-        return TWO && t ? sip_load(rsrc_b, base_b, o, 1u, ln, data_b) : sip_load(rsrc_a, base_a, o, 0u, ln, data_a);
-    };
+    // the first blocks' directory entries, then the payload windows' bases:
+    // all issued before any is waited on (one round trip, not two)
     const uint2 oA = next_offsets();
     SipRef rA = nr;
     const uint2 oB = next_offsets();
     SipRef rB = nr;
     uint2 oC = next_offsets();
     SipRef rC = nr;
+    uint2 oD = make_uint2(0u, 0u);
+    SipRef rD;
+    if constexpr (QUAD) {
+        oD = next_offsets();
+        rD = nr;
+    }
+    // each tensor's payload window: from the workgroup's first block of it
+    // (the raw twin: from the workgroup's first row, 512 words a block)
+    uint32_t base_a = 0, base_b = 0;
+    if constexpr (!RAW) {
+        base_a = ((const_u32_ptr)offsets_a)[sp.a_first];
+        base_b = ((const_u32_ptr)offsets_b)[0];
+    }
+    const i32x4 rsrc_a = make_rsrc(RAW ? data_a + (uint64_t)sp.a_first * 512u : data_a + base_a, 0x7FFFFFFFu);
+    const i32x4 rsrc_b = make_rsrc(data_b + base_b, 0x7FFFFFFFu);
+    const SipLanes ln = sip_lanes(lane);
+    auto load = [&](uint2 o, uint32_t t) {
+        if constexpr (RAW) return raw_load(rsrc_a, o.x, ln);
+        return TWO && t ? sip_load(rsrc_b, base_b, o, 1u, ln, data_b) : sip_load(rsrc_a, base_a, o, 0u, ln, data_a);
+    };
     // the prologue's stages issue in the loop's order (no interleaving),
     // so the waits the loop needs are the same on entry as in steady state
     SipStage sA = load(oA, rA.t);
@@ -838,14 +846,11 @@ void k_gemv_sip(const SipGroup g, const uint16_t* __restrict__ x, const SipShape
     // and 6% on 4096 x 4096; at M = 2, mixed)
     constexpr bool DEEP = M >= 4;
     SipStage sC, sD;
-    SipRef rD;
     if constexpr (DEEP) {
         sC = load(oC, rC.t);
         __builtin_amdgcn_sched_barrier(0);
     }
     if constexpr (QUAD) {  // (quad steps keep four blocks in flight: one step's)
-        const uint2 oD = next_offsets();
-        rD = nr;
         sD = load(oD, rD.t);
         __builtin_amdgcn_sched_barrier(0);
     }
@@ -1417,9 +1422,6 @@ void k_gemv_gulp(const SipGroup g, const uint16_t* __restrict__ x, const SipShap
         sip_start<false>(sh, p, wv, wk, sp);
         c = p;
     }
-    const uint32_t base = ((const_u32_ptr)offsets)[sp.a_first];
-    const i32x4 rsrc = make_rsrc(data + base, 0x7FFFFFFFu);
-    const GulpLanes ln = gulp_lanes(lane);
     uint32_t ns = 0;  // the schedule of the last next_offsets() block
     auto next_offsets = [&]() {
         const uint32_t blk = QUAD ? quad_issue<false>(sh, pq, sp, nrows).blk : sip_issue<false>(sh, p, sp).blk;
@@ -1431,12 +1433,23 @@ void k_gemv_gulp(const SipGroup g, const uint16_t* __restrict__ x, const SipShap
             sip_next<false>(sh, p, wk, sp);
         return o;
     };
+    // the first blocks' directory and schedule entries, then the payload
+    // window's base: all issued before any is waited on
     const uint2 oA = next_offsets();
     const uint32_t nA = ns;
     const uint2 oB = next_offsets();
     const uint32_t nB = ns;
     uint2 oC = next_offsets();
     uint32_t nC = ns;
+    uint2 oD0 = make_uint2(0u, 0u);
+    uint32_t nD0 = 0;
+    if constexpr (QUAD) {
+        oD0 = next_offsets();
+        nD0 = ns;
+    }
+    const uint32_t base = ((const_u32_ptr)offsets)[sp.a_first];
+    const i32x4 rsrc = make_rsrc(data + base, 0x7FFFFFFFu);
+    const GulpLanes ln = gulp_lanes(lane);
     GulpStage sA = gulp_load(rsrc, base, oA, nA, ln);
     __builtin_amdgcn_sched_barrier(0);
     GulpStage sB = gulp_load(rsrc, base, oB, nB, ln);
@@ -1445,8 +1458,7 @@ void k_gemv_gulp(const SipGroup g, const uint16_t* __restrict__ x, const SipShap
     if constexpr (QUAD) {  // (quad steps keep four blocks in flight: one step's)
         sC = gulp_load(rsrc, base, oC, nC, ln);
         __builtin_amdgcn_sched_barrier(0);
-        const uint2 oD = next_offsets();
-        sD = gulp_load(rsrc, base, oD, ns, ln);
+        sD = gulp_load(rsrc, base, oD0, nD0, ln);
         __builtin_amdgcn_sched_barrier(0);
     }
 
