@@ -1335,14 +1335,21 @@ __device__ __forceinline__ uint32_t gulp_field(const uint32_t* p, uint32_t i, ui
 
 // Builds the gulp tables of a palette (6 words: tier 0, tier 1, tier 2 x 4,
 // each entry list padded with a zero byte that the escape code reads):
-//   t0tab[c0 | c1 << 2 | c2 << 4 | c3 << 6]: E(c0) << 7 | E(c1) << 23 |
-//       m0 << 3 | 2 popcount(m0) << 15, and E(c2) << 7 | E(c3) << 23;
-//   t1tab[codes << 4 | m0]: the same for tier 1, the four codes taken in
-//       order by the escaped positions of m0 (others 0), with m1 (the
-//       positions whose tier-1 code escapes) << 3 | popcount(m1) << 15;
+//   t0tab[c0 | c1 << 2 | c2 << 4 | c3 << 6]: E(c0) << 7 | E(c1) << 23,
+//       E(c2) << 7 | E(c3) << 23, 2 popcount(m0) (the group's tier-1 bits)
+//       and 8 t1_base(m0) (the byte offset of m0's run of the tier-1
+//       table), each in a word of its own so that neither needs
+//       extracting;
+//   t1tab[t1_base(m0) + codes]: for a group whose tier-0 escapes are m0,
+//       its popcount(m0) tier-1 codes (2 bits each, in order) placed at the
+//       escaped positions: E << 7 | E << 23 pairs as tier 0's, with m1 (the
+//       positions whose tier-1 code escapes) << 3 | popcount(m1) << 15.
+//       m0 has 4^popcount(m0) code patterns, so the runs hold
+//       (1 + 4)^4 = 625 entries (a table indexed by m0 and four whole
+//       codes would hold 4096, mostly repeats).
 //   pal2[c]: tier 2's bytes.
 template <int THREADS>
-__device__ __forceinline__ void gulp_tables(uint2* t0tab, uint2* t1tab, uint8_t* pal2, const uint32_t* palette) {
+__device__ __forceinline__ void gulp_tables(uint4* t0tab, uint2* t1tab, uint8_t* pal2, const uint32_t* palette) {
     const const_u32_ptr pw = (const_u32_ptr)palette;
     const uint32_t p0 = pw[0], p1 = pw[1];
     for (uint32_t i = threadIdx.x; i < 256; i += THREADS) {
@@ -1352,11 +1359,12 @@ __device__ __forceinline__ void gulp_tables(uint2* t0tab, uint2* t1tab, uint8_t*
             e[k] = (p0 >> (8 * c)) & 0xFFu;
             m |= (c == 3u) << k;
         }
-        t0tab[i] = make_uint2((e[0] << 7) | (e[1] << 23) | (m << 3) | ((2u * __builtin_popcount(m)) << 15),
-                              (e[2] << 7) | (e[3] << 23));
+        t0tab[i] = make_uint4((e[0] << 7) | (e[1] << 23), (e[2] << 7) | (e[3] << 23), 2u * __builtin_popcount(m),
+                              8u * gulp_t1_base(m));
     }
-    for (uint32_t i = threadIdx.x; i < 4096; i += THREADS) {
-        const uint32_t m0 = i & 15u, codes = i >> 4;
+    for (uint32_t i = threadIdx.x; i < kGulpT1Entries; i += THREADS) {
+        uint32_t m0, codes;
+        gulp_t1_entry(i, m0, codes);
         uint32_t e[4], m1 = 0, r = 0;
         for (uint32_t k = 0; k < 4; ++k) {
             e[k] = 0;
@@ -1384,8 +1392,8 @@ void k_gemv_gulp(const SipGroup g, const uint16_t* __restrict__ x, const SipShap
     constexpr int W = kSipWaves, TH = kSipThreads;
     // verify rows four output rows at a time on the matrix cores
     constexpr bool QUAD = !DEC && gulp_quad(M);
-    __shared__ uint2 t0tab[256];
-    __shared__ uint2 t1tab[4096];
+    __shared__ uint4 t0tab[256];
+    __shared__ uint2 t1tab[kGulpT1Entries];
     __shared__ uint2 sel2[13 * 16];
     __shared__ uint32_t pal2w[4];
     __shared__ uint32_t x2_all[W * kGulpX2Words];
@@ -1518,10 +1526,10 @@ void k_gemv_gulp(const SipGroup g, const uint16_t* __restrict__ x, const SipShap
         const bool has_term = len > kGulpFixed + w1 + w2;
         // tier 0
         const uint32_t T0 = s0.t0;
-        uint2 E0 = t0tab[T0 & 0xFF];
-        uint2 E1 = t0tab[(T0 >> 8) & 0xFF];
-        uint2 E2 = t0tab[(T0 >> 16) & 0xFF];
-        uint2 E3 = t0tab[T0 >> 24];
+        const uint4 F0 = t0tab[T0 & 0xFF], F1 = t0tab[(T0 >> 8) & 0xFF], F2 = t0tab[(T0 >> 16) & 0xFF],
+                    F3 = t0tab[T0 >> 24];
+        uint2 E0 = make_uint2(F0.x, F0.y), E1 = make_uint2(F1.x, F1.y), E2 = make_uint2(F2.x, F2.y),
+              E3 = make_uint2(F3.x, F3.y);
         // lane j's two tier-2 codes (tier-1 escapes 2j, 2j + 1, in tier-2
         // word j / 4, the one it loaded) and their palette bytes: read now,
         // beside the tier-0 lookups
@@ -1533,8 +1541,7 @@ void k_gemv_gulp(const SipGroup g, const uint16_t* __restrict__ x, const SipShap
         const uint16_t* xb = xs + c.cb * 1024 + 8 * lane;
         uint4 xa, xc;
         // twice the tier-0 escapes of each group, and their prefix in the lane
-        const uint32_t h0 = (E0.x >> 15) & 15u, h1 = (E1.x >> 15) & 15u, h2 = (E2.x >> 15) & 15u;
-        const uint32_t o1 = h0, o2 = o1 + h1, o3 = o2 + h2, cnt1 = (o3 + ((E3.x >> 15) & 15u)) >> 1;
+        const uint32_t o1 = F0.z, o2 = o1 + F1.z, o3 = o2 + F2.z, cnt1 = (o3 + F3.z) >> 1;
         const uint32_t q0 = wave_scan_incl_dpp(cnt1) - cnt1;
         // tier 1: the lane's codes, 2 bits each from bit 2 q0 of the stream
         const int k1 = (int)((q0 >> 2) & ~3u);
@@ -1554,8 +1561,12 @@ void k_gemv_gulp(const SipGroup g, const uint16_t* __restrict__ x, const SipShap
                          : "memory");
         }
         const uint32_t W1 = __builtin_amdgcn_alignbit(v1, v0, (q0 & 15u) << 1);
-#define DMX_T1(E, off) t1tab[(__builtin_amdgcn_ubfe(W1, (off), 8) << 4) | ((E.x >> 3) & 15u)]
-        const uint2 P0 = DMX_T1(E0, 0u), P1 = DMX_T1(E1, o1), P2 = DMX_T1(E2, o2), P3 = DMX_T1(E3, o3);
+        // (the group's 2 popcount(m0) code bits from bit off, at byte
+        // offset 8 t1_base(m0) + 8 codes)
+#define DMX_T1(F, off)                                                                              \
+    *reinterpret_cast<const uint2*>(reinterpret_cast<const uint8_t*>(t1tab) +                       \
+                                    ((__builtin_amdgcn_ubfe(W1, (off), F.z) << 3) + F.w))
+        const uint2 P0 = DMX_T1(F0, 0u), P1 = DMX_T1(F1, o1), P2 = DMX_T1(F2, o2), P3 = DMX_T1(F3, o3);
 #undef DMX_T1
         E0.x |= P0.x & 0x7F807F80u;
         E0.y |= P0.y;
@@ -1625,8 +1636,14 @@ void k_gemv_gulp(const SipGroup g, const uint16_t* __restrict__ x, const SipShap
             // lane j resolves tier-1 escapes 2j, 2j + 1 (codes ca, cb), code 15
             // escaping to the terminal
             uint32_t ea = pa, eb = pb;
-            const bool ta = 2 * lane < n2 && ca == 15u, tb = 2 * lane + 1 < n2 && cb == 15u;
-            if (__builtin_amdgcn_ballot_w64(ta || tb) != 0 && has_term) {
+            // (has_term, uniform and false unless the block has a terminal
+            // stream, is tested first: then the per-lane tests are skipped)
+            bool ta = false, tb = false;
+            if (has_term) {
+                ta = 2 * lane < n2 && ca == 15u;
+                tb = 2 * lane + 1 < n2 && cb == 15u;
+            }
+            if (has_term && __builtin_amdgcn_ballot_w64(ta || tb) != 0) {
                 const uint32_t nt = (uint32_t)ta + (uint32_t)tb;
                 const uint32_t inc3 = wave_scan_incl(nt), q3 = inc3 - nt;
                 // terminal byte r is byte r & 3 of word r >> 2, held by lane r >> 2

@@ -56,14 +56,38 @@ constexpr size_t kLdsBytes = 160 * 1024;    // LDS of one CU
 constexpr uint32_t kSipPerCu = 1, kGulpPerCu = 2, kDecodePerCu = 2;
 
 // Static LDS of the sip and gulp kernels (their tables), for the plans: sip
-// its 4096-entry exponent table and its selector tables; gulp its tier-0
-// and tier-1 tables, selectors, the tier-2 palette and each wave's exponent
-// byte exchange.
+// its 4096-entry exponent table, its selector tables and its progress
+// counter (4 bytes, 16 with alignment); gulp its tier-0 and tier-1 tables,
+// selectors, the tier-2 palette and each wave's exponent byte exchange.
 constexpr uint32_t kSelBytes = (16 + 13 * 16) * 8;
-constexpr uint32_t kGulpT0Bytes = 256 * 8;
+constexpr uint32_t kGulpT0Bytes = 256 * 16;
+// gulp's tier-1 table: for each tier-0 escape mask m0 of a group of four
+// weights, a run of 4^popcount(m0) entries (its tier-1 code patterns), the
+// runs in order of m0: 625 entries of 8 bytes. m0's run starts after those
+// of the masks below it; the ones that first differ from m0 at its set bit
+// k are 2^k masks with 4^popcount(m0 above k) 5^k patterns in all.
+DMX_HD constexpr uint32_t gulp_t1_base(uint32_t m0) {
+    uint32_t b = 0, p5 = 1;
+    for (uint32_t k = 0; k < 5; ++k, p5 *= 5)
+        if ((m0 >> k) & 1u) b += p5 << (2 * __builtin_popcount(m0 >> (k + 1)));
+    return b;
+}
+constexpr uint32_t kGulpT1Entries = 625;
+static_assert(gulp_t1_base(16) == kGulpT1Entries, "the runs of the gulp tier-1 table");
+// the inverse: entry i < 625 of the table is m0's entry `codes` (a running
+// sum over the runs, at most 16 steps)
+DMX_HD void gulp_t1_entry(uint32_t i, uint32_t& m0, uint32_t& codes) {
+    uint32_t base = 0, run = 1;
+    m0 = 0;
+    while (i >= base + run) {
+        base += run;
+        run = 1u << (2 * __builtin_popcount(++m0));
+    }
+    codes = i - base;
+}
 constexpr uint32_t kGulpX2Words = 40;  // per wave: 128 exponent bytes + a window's overhang
-constexpr size_t kSipStaticLds = kTableBytes + kSelBytes;
-constexpr size_t kGulpStaticLds = kGulpT0Bytes + kTableBytes + 13 * 16 * 8 + 16 + kPlanWaves * kGulpX2Words * 4;
+constexpr size_t kSipStaticLds = kTableBytes + kSelBytes + 16;
+constexpr size_t kGulpStaticLds = kGulpT0Bytes + ((kGulpT1Entries * 8 + 15) & ~15u) + 13 * 16 * 8 + 16 + kPlanWaves * kGulpX2Words * 4;
 
 // Verify rows in quad units: four output rows contracted at once on the
 // matrix cores, sip at M = 4 and 8, gulp at M = 8. The quad path holds four

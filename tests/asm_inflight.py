@@ -176,15 +176,20 @@ def kernels(asm: str, pattern: str):
 
 def metadata(asm: str) -> dict:
     """-> {kernel name: {vgpr_count, sgpr_count, vgpr_spill_count,
-    sgpr_spill_count, private_segment_fixed_size}} from the code object's
-    metadata block of an assembly file."""
+    sgpr_spill_count, private_segment_fixed_size, group_segment_fixed_size}}
+    from the code object's metadata block of an assembly file (one entry of
+    its kernel list per kernel, the keys in any order)."""
     out = {}
-    for m in re.finditer(r"\.name:\s+(_Z\S+)\n(.*?)(?=\n\s+- \.|\n\.end_amdgpu_metadata)", asm, re.S):
+    block = asm[asm.find(".amdgpu_metadata"):asm.find(".end_amdgpu_metadata")]
+    for entry in re.split(r"\n  - \.", block)[1:]:
+        name = re.search(r"\.name:\s+(_Z\S+)", entry)
+        if not name:
+            continue
         fields = {}
         for key in ("vgpr_count", "sgpr_count", "vgpr_spill_count", "sgpr_spill_count",
-                    "private_segment_fixed_size"):
-            mm = re.search(r"\." + key + r":\s+(\d+)", m.group(2))
+                    "private_segment_fixed_size", "group_segment_fixed_size"):
+            mm = re.search(r"(?:^|\s)\.?" + key + r":\s+(\d+)", entry)
             if mm:
                 fields[key] = int(mm.group(1))
-        out[m.group(1)] = fields
+        out[name.group(1)] = fields
     return out

@@ -225,3 +225,38 @@ def test_no_scratch_and_no_vgpr_spill_in_kernels_with_untracked_loads(kernel_asm
         sgpr_spills[name] = md[name].get("sgpr_spill_count", 0)
         assert body.count("v_writelane_b32") >= sgpr_spills[name] > 0 or sgpr_spills[name] == 0
     print("SGPR spills (to VGPR lanes):", {k[20:60]: v for k, v in sgpr_spills.items() if v})
+
+
+def _plan_constants(tmp_path):
+    """kSipStaticLds and kGulpStaticLds as the host's plans use them."""
+    src = tmp_path / "lds.cpp"
+    src.write_text('#include <cstdio>\n#include "plan.h"\n'
+                   'int main() { printf("%zu %zu\\n", dmx::kSipStaticLds, dmx::kGulpStaticLds); }\n')
+    exe = tmp_path / "lds"
+    subprocess.run(["g++", "-std=c++17", "-I", os.path.join(ROOT, "drinkme_amd", "csrc"), str(src), "-o", str(exe)],
+                   check=True, timeout=120)
+    sip, gulp = (int(v) for v in subprocess.run([str(exe)], capture_output=True, text=True,
+                                                 check=True).stdout.split())
+    return sip, gulp
+
+
+def test_static_lds_fits_what_the_plans_reserve(kernel_asm, tmp_path):
+    """The host plans a launch's dynamic LDS (activation rows, row partials)
+    around the kernels' static tables: a kernel whose static LDS outgrew
+    the reserved figure would leave the plan's two workgroups per CU (or its
+    column phases) unable to fit, and fail to launch. Each sip and gulp
+    kernel's group segment, from its code-object metadata, fits in its
+    family's figure."""
+    from tests.asm_inflight import metadata
+
+    sip_lds, gulp_lds = _plan_constants(tmp_path)
+    md = metadata(kernel_asm)
+    seen = 0
+    for name, fields in md.items():
+        fam = "gulp" if "k_gemv_gulp" in name else "sip" if "k_gemv_sip" in name else None
+        if fam is None:
+            continue
+        seen += 1
+        limit = gulp_lds if fam == "gulp" else sip_lds
+        assert fields["group_segment_fixed_size"] <= limit, (name, fields["group_segment_fixed_size"], limit)
+    assert seen == 34

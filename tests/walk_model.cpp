@@ -246,9 +246,32 @@ uint32_t rnd(uint32_t n) {
 
 }  // namespace
 
+// gulp's tier-1 table (625 entries in LDS, no bounds check on its reads):
+// every (m0, codes) the kernel can look up, codes < 4^popcount(m0), lies
+// in the table, each entry is one pair's, and the table build's inverse
+// maps each entry back to its pair.
+void check_gulp_t1() {
+    std::vector<int> hit(kGulpT1Entries, 0);
+    for (uint32_t m0 = 0; m0 < 16; ++m0)
+        for (uint32_t c = 0; c < (1u << (2 * __builtin_popcount(m0))); ++c) {
+            const uint32_t i = gulp_t1_base(m0) + c;
+            if (i >= kGulpT1Entries) {
+                bad("gulp tier-1 index " + std::to_string(i) + " past the table");
+                continue;
+            }
+            ++hit[i];
+            uint32_t m, k;
+            gulp_t1_entry(i, m, k);
+            if (m != m0 || k != c) bad("gulp tier-1 entry " + std::to_string(i) + " maps back wrong");
+        }
+    for (uint32_t i = 0; i < kGulpT1Entries; ++i)
+        if (hit[i] != 1) bad("gulp tier-1 entry " + std::to_string(i) + " held by " + std::to_string(hit[i]));
+}
+
 int main(int argc, char** argv) {
     if (argc == 3 && !strcmp(argv[1], "--plant")) g_plant = atoi(argv[2]);
     check_reach();
+    check_gulp_t1();
     // the configurations' launches: Qwen3-8B (q/k/v, o, gate/up, down,
     // lm_head) and the 32B class, grouped as the benchmark groups them
     const std::vector<std::pair<std::vector<uint32_t>, uint32_t>> shapes = {
