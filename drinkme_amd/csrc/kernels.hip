@@ -1334,7 +1334,9 @@ __device__ __forceinline__ uint32_t gulp_field(const uint32_t* p, uint32_t i, ui
 }
 
 // Builds the gulp tables of a palette (6 words: tier 0, tier 1, tier 2 x 4,
-// each entry list padded with a zero byte that the escape code reads):
+// each entry list padded with a zero byte that the escape code reads; the
+// entries are plan.h's gulp_t0_entry and gulp_t1_value, which the host
+// model of the walk checks against a direct decode of every code):
 //   t0tab[c0 | c1 << 2 | c2 << 4 | c3 << 6]: E(c0) << 7 | E(c1) << 23,
 //       E(c2) << 7 | E(c3) << 23, 2 popcount(m0) (the group's tier-1 bits)
 //       and 8 t1_base(m0) (the byte offset of m0's run of the tier-1
@@ -1353,29 +1355,14 @@ __device__ __forceinline__ void gulp_tables(uint4* t0tab, uint2* t1tab, uint8_t*
     const const_u32_ptr pw = (const_u32_ptr)palette;
     const uint32_t p0 = pw[0], p1 = pw[1];
     for (uint32_t i = threadIdx.x; i < 256; i += THREADS) {
-        uint32_t e[4], m = 0;
-        for (uint32_t k = 0; k < 4; ++k) {
-            const uint32_t c = (i >> (2 * k)) & 3u;
-            e[k] = (p0 >> (8 * c)) & 0xFFu;
-            m |= (c == 3u) << k;
-        }
-        t0tab[i] = make_uint4((e[0] << 7) | (e[1] << 23), (e[2] << 7) | (e[3] << 23), 2u * __builtin_popcount(m),
-                              8u * gulp_t1_base(m));
+        uint32_t f[4];
+        gulp_t0_entry(p0, i, f);
+        t0tab[i] = make_uint4(f[0], f[1], f[2], f[3]);
     }
     for (uint32_t i = threadIdx.x; i < kGulpT1Entries; i += THREADS) {
-        uint32_t m0, codes;
-        gulp_t1_entry(i, m0, codes);
-        uint32_t e[4], m1 = 0, r = 0;
-        for (uint32_t k = 0; k < 4; ++k) {
-            e[k] = 0;
-            if ((m0 >> k) & 1u) {
-                const uint32_t c = (codes >> (2 * r++)) & 3u;
-                e[k] = (p1 >> (8 * c)) & 0xFFu;
-                m1 |= (c == 3u) << k;
-            }
-        }
-        t1tab[i] = make_uint2((e[0] << 7) | (e[1] << 23) | (m1 << 3) | ((uint32_t)__builtin_popcount(m1) << 15),
-                              (e[2] << 7) | (e[3] << 23));
+        uint32_t v[2];
+        gulp_t1_value(p1, i, v);
+        t1tab[i] = make_uint2(v[0], v[1]);
     }
     // (uniform scalar reads: a vector load here would need a vmcnt(0) wait,
     // which would also wait out the payload loads already in flight)
@@ -1563,9 +1550,8 @@ void k_gemv_gulp(const SipGroup g, const uint16_t* __restrict__ x, const SipShap
         const uint32_t W1 = __builtin_amdgcn_alignbit(v1, v0, (q0 & 15u) << 1);
         // (the group's 2 popcount(m0) code bits from bit off, at byte
         // offset 8 t1_base(m0) + 8 codes)
-#define DMX_T1(F, off)                                                                              \
-    *reinterpret_cast<const uint2*>(reinterpret_cast<const uint8_t*>(t1tab) +                       \
-                                    ((__builtin_amdgcn_ubfe(W1, (off), F.z) << 3) + F.w))
+#define DMX_T1(F, off) \
+    *reinterpret_cast<const uint2*>(reinterpret_cast<const uint8_t*>(t1tab) + gulp_t1_byte(W1, (off), F.z, F.w))
         const uint2 P0 = DMX_T1(F0, 0u), P1 = DMX_T1(F1, o1), P2 = DMX_T1(F2, o2), P3 = DMX_T1(F3, o3);
 #undef DMX_T1
         E0.x |= P0.x & 0x7F807F80u;

@@ -85,6 +85,53 @@ DMX_HD void gulp_t1_entry(uint32_t i, uint32_t& m0, uint32_t& codes) {
     }
     codes = i - base;
 }
+
+// The gulp tables' entries, built by the kernels in LDS from the palette's
+// tier-0 word p0 and tier-1 word p1 (bytes 0..2 the entries, byte 3 the
+// zero that an escape code reads).
+// Tier-0 entry i, four 2-bit codes c_k = (i >> 2k) & 3: E(c0) << 7 |
+// E(c1) << 23, E(c2) << 7 | E(c3) << 23 (the bf16 pairs' exponent fields),
+// 2 popcount(m0) and 8 t1_base(m0), m0 the positions whose code is 3.
+DMX_HD void gulp_t0_entry(uint32_t p0, uint32_t i, uint32_t (&f)[4]) {
+    uint32_t e[4], m = 0;
+    for (uint32_t k = 0; k < 4; ++k) {
+        const uint32_t c = (i >> (2 * k)) & 3u;
+        e[k] = (p0 >> (8 * c)) & 0xFFu;
+        m |= (uint32_t)(c == 3u) << k;
+    }
+    f[0] = (e[0] << 7) | (e[1] << 23);
+    f[1] = (e[2] << 7) | (e[3] << 23);
+    f[2] = 2u * (uint32_t)__builtin_popcount(m);
+    f[3] = 8u * gulp_t1_base(m);
+}
+// Tier-1 entry i (m0's entry `codes`): its popcount(m0) codes, 2 bits each
+// in order, at the positions of m0, as the same exponent pairs, with m1 (the
+// positions whose tier-1 code is 3) << 3 | popcount(m1) << 15 in the first.
+DMX_HD void gulp_t1_value(uint32_t p1, uint32_t i, uint32_t (&v)[2]) {
+    uint32_t m0, codes;
+    gulp_t1_entry(i, m0, codes);
+    uint32_t e[4], m1 = 0, r = 0;
+    for (uint32_t k = 0; k < 4; ++k) {
+        e[k] = 0;
+        if ((m0 >> k) & 1u) {
+            const uint32_t c = (codes >> (2 * r++)) & 3u;
+            e[k] = (p1 >> (8 * c)) & 0xFFu;
+            m1 |= (uint32_t)(c == 3u) << k;
+        }
+    }
+    v[0] = (e[0] << 7) | (e[1] << 23) | (m1 << 3) | ((uint32_t)__builtin_popcount(m1) << 15);
+    v[1] = (e[2] << 7) | (e[3] << 23);
+}
+// A group's tier-1 entry, as a byte offset in the table: its f2 = 2
+// popcount(m0) code bits from bit `off` of the lane's tier-1 window w1 (a
+// v_bfe: width 0 reads 0), in the run at byte f3 (f2, f3: its tier-0 entry's)
+DMX_HD uint32_t gulp_t1_byte(uint32_t w1, uint32_t off, uint32_t f2, uint32_t f3) {
+#ifdef __HIP_DEVICE_COMPILE__
+    return (__builtin_amdgcn_ubfe(w1, off, f2) << 3) + f3;
+#else
+    return ((f2 ? (w1 >> off) & (0xFFFFFFFFu >> (32 - f2)) : 0u) << 3) + f3;
+#endif
+}
 constexpr uint32_t kGulpX2Words = 40;  // per wave: 128 exponent bytes + a window's overhang
 constexpr size_t kSipStaticLds = kTableBytes + kSelBytes + 16;
 constexpr size_t kGulpStaticLds = kGulpT0Bytes + ((kGulpT1Entries * 8 + 15) & ~15u) + 13 * 16 * 8 + 16 + kPlanWaves * kGulpX2Words * 4;

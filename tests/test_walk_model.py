@@ -9,7 +9,11 @@ right partial, is the walk. The model plans every configuration's launches
 (the Qwen3-8B and 32B-class groups, lm_head, small and ragged groups, six
 hundred seeded random groups) for the sip, gulp, decode and raw-twin kernels
 at M = 1..8 and three CU counts, and walks every wave of every workgroup,
-past its work as far as a load pipeline runs ahead. The four planted
+past its work as far as a load pipeline runs ahead. It also decodes every
+code pattern through the gulp tables as the kernel looks them up (the
+tables' entries and lookup are plan.h's, shared with the kernel) against a
+direct decode: a layout mistake there only sends blocks down the exact
+fallback, correct but slow, so no parity test would see it. The five planted
 mistakes are its negative controls: each must be caught."""
 
 import os
@@ -38,7 +42,7 @@ def test_every_walk_stays_in_range_and_covers_each_block_once(model):
     assert plans > 500
 
 
-@pytest.mark.parametrize("plant", [1, 2, 3, 4])
+@pytest.mark.parametrize("plant", [1, 2, 3, 4, 5])
 def test_planted_walk_mistakes_are_caught(model, plant):
     res = subprocess.run([model, "--plant", str(plant)], capture_output=True, text=True, timeout=300)
     assert res.returncode == 0 and "caught" in res.stdout and "NOT" not in res.stdout, res.stdout + res.stderr

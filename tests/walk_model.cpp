@@ -268,10 +268,68 @@ void check_gulp_t1() {
         if (hit[i] != 1) bad("gulp tier-1 entry " + std::to_string(i) + " held by " + std::to_string(hit[i]));
 }
 
+// gulp's tables as the kernel looks them up, against a direct decode of
+// the codes: for seeded palettes, every tier-0 pattern and every tier-1 code
+// pattern of its escapes, the codes placed at an even offset of a random
+// window. The exponent fields of tier 0 | tier 1 must be the palette entries
+// at the positions that do not escape twice, zero at those that do; m1 and
+// its count must name those; the tier-1 bit count must be 2 popcount(m0).
+// (Planted mistake 5: the runs' byte offsets at 16 bytes an entry.)
+void check_gulp_tables() {
+    uint64_t rng = 0x243F6A8885A308D3ull;
+    auto next = [&]() {
+        rng = rng * 6364136223846793005ull + 1442695040888963407ull;
+        return (uint32_t)(rng >> 32);
+    };
+    for (int pal = 0; pal < 64; ++pal) {
+        const uint32_t p0 = next() & 0x00FFFFFFu, p1 = next() & 0x00FFFFFFu;  // byte 3: the escape's zero
+        for (uint32_t i = 0; i < 256; ++i) {
+            uint32_t f[4];
+            gulp_t0_entry(p0, i, f);
+            if (g_plant == 5) f[3] *= 2;
+            uint32_t m0 = 0;
+            for (uint32_t k = 0; k < 4; ++k) m0 |= (uint32_t)(((i >> (2 * k)) & 3u) == 3u) << k;
+            const uint32_t n1 = (uint32_t)__builtin_popcount(m0);
+            if (f[2] != 2 * n1) bad("gulp tier-0 entry " + std::to_string(i) + ": tier-1 bit count");
+            for (uint32_t codes = 0; codes < (1u << (2 * n1)); ++codes) {
+                const uint32_t off = 2 * (next() % (17 - n1));  // the group's bits end by bit 32
+                uint32_t w1 = next();
+                if (n1) w1 = (w1 & ~(((1u << (2 * n1)) - 1u) << off)) | (codes << off);
+                const uint32_t byte = gulp_t1_byte(w1, off, f[2], f[3]);
+                if (byte % 8 || byte / 8 >= kGulpT1Entries) {
+                    bad("gulp tier-1 lookup " + std::to_string(byte) + " outside the table");
+                    continue;
+                }
+                uint32_t v[2];
+                gulp_t1_value(p1, byte / 8, v);
+                uint32_t want[2] = {0, 0}, m1 = 0, r = 0;
+                for (uint32_t k = 0; k < 4; ++k) {
+                    const uint32_t c0 = (i >> (2 * k)) & 3u;
+                    uint32_t e = (p0 >> (8 * c0)) & 0xFFu;
+                    if (c0 == 3u) {
+                        const uint32_t c1 = (codes >> (2 * r++)) & 3u;
+                        e = c1 == 3u ? 0u : (p1 >> (8 * c1)) & 0xFFu;
+                        m1 |= (uint32_t)(c1 == 3u) << k;
+                    }
+                    want[k / 2] |= e << (k % 2 ? 23 : 7);
+                }
+                const uint32_t ex = 0x7F807F80u;
+                if (((f[0] | v[0]) & ex) != want[0] || ((f[1] | v[1]) & ex) != want[1] ||
+                    ((v[0] >> 3) & 15u) != m1 || ((v[0] >> 15) & 7u) != (uint32_t)__builtin_popcount(m1)) {
+                    bad("gulp tables: tier-0 pattern " + std::to_string(i) + ", tier-1 codes " +
+                        std::to_string(codes) + " decode wrong");
+                    return;
+                }
+            }
+        }
+    }
+}
+
 int main(int argc, char** argv) {
     if (argc == 3 && !strcmp(argv[1], "--plant")) g_plant = atoi(argv[2]);
     check_reach();
     check_gulp_t1();
+    check_gulp_tables();
     // the configurations' launches: Qwen3-8B (q/k/v, o, gate/up, down,
     // lm_head) and the 32B class, grouped as the benchmark groups them
     const std::vector<std::pair<std::vector<uint32_t>, uint32_t>> shapes = {
