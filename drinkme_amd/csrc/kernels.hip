@@ -1260,13 +1260,16 @@ void k_gemv_sip(const SipGroup g, const uint16_t* __restrict__ x, const SipShape
 // The work split, load pipeline and products are the sip kernel's. Lane l
 // owns weights 16l .. 16l + 15; per group of four weights:
 //   tier 0  a 256-entry LDS table indexed by the four codes gives the
-//           exponents of the resolved weights and the escape mask m0;
+//           exponents of the resolved weights, the group's tier-1 bit count
+//           2 popcount(m0) (m0: its escape mask) and m0's run in the tier-1
+//           table;
 //   tier 1  the lane's tier-1 codes are a 32-bit window of the tier-1
 //           stream at bit 2 q0 (q0: the wave's exclusive prefix of tier-0
 //           escape counts), pulled from the lanes holding it (lane j holds
-//           tier-1 word j); a 4096-entry table indexed by (the group's next
-//           four codes, m0) gives the tier-1 exponents at the escaped
-//           positions and the tier-1 escape mask m1;
+//           tier-1 word j); the group's entry in m0's run of the 625-entry
+//           tier-1 table, at its 2 popcount(m0) code bits, gives the tier-1
+//           exponents at the escaped positions and the tier-1 escape mask
+//           m1;
 //   tier 2  lane j resolves tier-1 escapes 2j and 2j + 1 of the block from
 //           the tier-2 word it loaded (and the terminal, for code 15) and
 //           writes their exponent bytes to the wave's LDS array; each lane
