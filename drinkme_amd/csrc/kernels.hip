@@ -553,9 +553,11 @@ struct SipStage {
 // address space its wave-uniform reads become scalar loads.
 typedef const __attribute__((address_space(4))) uint32_t* const_u32_ptr;
 
-// A block's directory pair, read through the scalar cache.
+// A block's directory pair, read through the scalar cache. (The byte
+// offset is 32-bit, so the load takes it in an SGPR with no 64-bit address
+// add: the fast kernels run tensors of fewer than 2^30 blocks.)
 __device__ __forceinline__ uint2 sip_offsets(const uint32_t* offsets, uint32_t blk) {
-    const const_u32_ptr p = (const_u32_ptr)(offsets + blk);
+    const const_u32_ptr p = (const_u32_ptr)(reinterpret_cast<const char*>(offsets) + blk * 4u);
     return make_uint2(p[0], p[1]);
 }
 
@@ -1424,7 +1426,8 @@ void k_gemv_gulp(const SipGroup g, const uint16_t* __restrict__ x, const SipShap
     auto next_offsets = [&]() {
         const uint32_t blk = QUAD ? quad_issue<false>(sh, pq, sp, nrows).blk : sip_issue<false>(sh, p, sp).blk;
         const uint2 o = sip_offsets(offsets, blk);
-        ns = (((const_u32_ptr)sched)[blk >> 1] >> ((blk & 1u) * 16)) & 0xFFFFu;
+        ns = (*(const_u32_ptr)(reinterpret_cast<const char*>(sched) + ((blk * 2u) & ~3u)) >> ((blk & 1u) * 16)) &
+             0xFFFFu;
         if constexpr (QUAD)
             quad_next(sh, pq, wk);
         else
@@ -2082,9 +2085,18 @@ SipKernel sip_kernel(int kind, int mi) {
 // One launch of the sip kernel over n tensors of equal cols (already
 // checked). Returns 2 when the group cannot run as one launch (a row tile
 // taller than a tensor, or tables past the LDS), having launched nothing.
+// The fast kernels address a tensor's directory with 32-bit byte offsets:
+// tensors of 2^30 blocks or more (a trillion weights) run on the generic
+// kernel.
+bool fast_directory(const dmx_radix_tensor* t) {
+    return (uint64_t)t->rows * ((t->cols + 1023) / 1024) < (1ull << 30);
+}
+
 int launch_sip(const dmx_radix_tensor* const* ts, uint32_t n, const void* x, uint32_t m, const void* const* bias,
                int bias_dtype, void* const* out, int out_dtype, hipStream_t stream, char* err, size_t errn) {
     if (n < 1 || n > (uint32_t)kGroupMax || m < 1 || m > 8) return 2;
+    for (uint32_t i = 0; i < n; ++i)
+        if (!fast_directory(ts[i])) return 2;
     const int mi = m == 1 ? 0 : m == 2 ? 1 : m <= 4 ? 2 : 3;
     const uint32_t M = 1u << mi;
     SipGroup g;
@@ -2158,6 +2170,8 @@ GulpKernel gulp_kernel(bool phased, int mi) {
 int launch_gulp(const dmx_radix_tensor* const* ts, uint32_t n, const void* x, uint32_t m, const void* const* bias,
                 int bias_dtype, void* const* out, int out_dtype, hipStream_t stream, char* err, size_t errn) {
     if (n < 1 || n > (uint32_t)kGroupMax || m < 1 || m > 8) return 2;
+    for (uint32_t i = 0; i < n; ++i)
+        if (!fast_directory(ts[i])) return 2;
     const int mi = m == 1 ? 0 : m == 2 ? 1 : m <= 4 ? 2 : 3;
     const uint32_t M = 1u << mi;
     SipGroup g;
@@ -2279,7 +2293,7 @@ int launch_decode_fast(const dmx_radix_tensor* t, uint16_t* out, hipStream_t str
     const bool sip = is_sip(t);
     const bool gulp = is_gulp(t) && t->schedule && (reinterpret_cast<uintptr_t>(t->schedule) & 3u) == 0;
     if (g_policy.load() != DMX_POLICY_AUTO || !(sip || gulp) || t->block_size != 1024 || t->cols % 1024 != 0 ||
-        (reinterpret_cast<uintptr_t>(out) & 15u) != 0)
+        (reinterpret_cast<uintptr_t>(out) & 15u) != 0 || !fast_directory(t))
         return 2;
     SipGroup g;
     SipShape sh;
