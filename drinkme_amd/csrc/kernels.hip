@@ -2131,7 +2131,8 @@ int launch_sip(const dmx_radix_tensor* const* ts, uint32_t n, const void* x, uin
     uint32_t grid = 0;
     size_t lds = 0;
     bool two = false;
-    if (!plan_launch(sh, g.row0, n, min_rows, M, kSipWaves, kSipPerCu, sip_quad((int)M), fixed, true,
+    if (!plan_launch(sh, g.row0, n, min_rows, M, kSipWaves, kSipPerCu, sip_quad((int)M),
+                     unit_end_cost(false, (int)M, false), fixed, true,
                      (uint32_t)cu_count(), grid, lds, two))
         return 2;
     {
@@ -2206,7 +2207,8 @@ int launch_gulp(const dmx_radix_tensor* const* ts, uint32_t n, const void* x, ui
     uint32_t grid = 0;
     size_t lds = 0;
     bool two = false;
-    if (!plan_launch(sh, g.row0, n, min_rows, M, kSipWaves, gulp_per_cu((int)M), gulp_quad((int)M), fixed, false,
+    if (!plan_launch(sh, g.row0, n, min_rows, M, kSipWaves, gulp_per_cu((int)M), gulp_quad((int)M),
+                     unit_end_cost(true, (int)M, false), fixed, false,
                      (uint32_t)cu_count(), grid, lds, two))
         return 2;
     {
@@ -2318,7 +2320,8 @@ int launch_decode_fast(const dmx_radix_tensor* t, uint16_t* out, hipStream_t str
     uint32_t grid = 0;
     size_t lds = 0;
     bool two = false;
-    if (!plan_launch(sh, g.row0, 1, t->rows, 1, kSipWaves, kDecodePerCu, false, fixed, sip, (uint32_t)cu_count(),
+    if (!plan_launch(sh, g.row0, 1, t->rows, 1, kSipWaves, kDecodePerCu, false, unit_end_cost(!sip, 1, true), fixed,
+                     sip, (uint32_t)cu_count(),
                      grid, lds, two) ||
         sh.phases > 1)
         return 2;
@@ -2482,7 +2485,7 @@ int launch_raw(const uint16_t* w, uint32_t rows, uint32_t cols, bool gulp, const
     size_t lds = 0;
     bool two = false;
     if (!plan_launch(sh, g.row0, 1, rows, M, kSipWaves, gulp ? gulp_per_cu((int)M) : kSipPerCu,
-                     gulp ? gulp_quad((int)M) : sip_quad((int)M), fixed,
+                     gulp ? gulp_quad((int)M) : sip_quad((int)M), unit_end_cost(gulp, (int)M, false), fixed,
                      !gulp, (uint32_t)cu_count(), grid, lds,
                      two))
         return 2;

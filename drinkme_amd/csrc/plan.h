@@ -409,14 +409,28 @@ constexpr uint32_t kGulpT1Max = 64, kGulpT2Max = 128;  // the clamps of a schedu
 
 // ---- the plan (host)
 
+// What the planner charges a unit's end, per activation row, in blocks: a
+// quarter for sip, for the quad units and for the decode (which stores its
+// blocks and sums nothing); a whole block for gulp's v_dot2 path, whose
+// blocks are bound by instruction issue and whose unit end (the wave's
+// sum, its LDS write and the cursor's step) is some 60 instructions: with
+// it the Qwen3-8B q/k/v and o run whole rows as units (the Qwen3-8B gulp
+// layer 1.1-1.4% faster at M = 1 and 1.0-2.1% at M = 4, the 32B-class
+// layer 0.5-1.9% at M = 1, over two A/B runs); charging the quad units so
+// made M = 8 9% slower.
+DMX_HD constexpr double unit_end_cost(bool gulp, int M, bool decode) {
+    return gulp && !decode && !gulp_quad(M) ? 1.0 : 0.25;
+}
+
 // The work plan of a sip or gulp launch over the group's sh.rows rows (row0:
 // the tensors' first rows, row0[n] = sh.rows): up to max_per_cu workgroups
 // per CU where their LDS fits, else fewer (M = 8's registers allow only
 // one); T rows per workgroup (quad mode: a multiple of four); the fewest
 // column phases P (a divisor of NB) whose activation slice fits in LDS;
 // within a phase, the segments that give the fewest block-times per
-// workgroup (a unit's closing sum, one per activation row, costing about a
-// quarter of a block). W is the kernel's waves per workgroup, quad whether
+// workgroup (a unit's closing sum and cursor step, per activation row,
+// costing `unit_cost` of a block: unit_end_cost()). W is the kernel's waves
+// per workgroup, quad whether
 // its verify rows run in quad units, `fixed` its static LDS; a second
 // exponent table is added when a tile spans two tensors (allowed only with
 // `allow_two`). Without it, a group whose tensor boundaries the even tile
@@ -425,8 +439,8 @@ constexpr uint32_t kGulpT1Max = 64, kGulpT2Max = 128;  // the clamps of a schedu
 // the resident ones run as a later round). Returns false, planning nothing,
 // when no plan fits.
 inline bool plan_launch(SipShape& sh, const uint32_t* row0, uint32_t n, uint32_t min_rows, uint32_t M, uint32_t W,
-                        uint32_t max_per_cu, bool quad, size_t fixed, bool allow_two, uint32_t cus, uint32_t& grid_out,
-                        size_t& lds_out, bool& two_out) {
+                        uint32_t max_per_cu, bool quad, double unit_cost, size_t fixed, bool allow_two, uint32_t cus,
+                        uint32_t& grid_out, size_t& lds_out, bool& two_out) {
     for (uint32_t per_cu = M == 8 ? 1 : max_per_cu; per_cu >= 1; --per_cu) {
         uint32_t grid = std::min<uint32_t>(sh.rows, cus * per_cu);
         uint32_t T = (sh.rows + grid - 1) / grid;
@@ -464,7 +478,7 @@ inline bool plan_launch(SipShape& sh, const uint32_t* row0, uint32_t n, uint32_t
                 for (uint32_t s = 1; s <= std::min<uint32_t>(K, W); ++s) {
                     if (K % s) continue;
                     const double rounds = std::ceil((double)urows * s / W);
-                    const double cost = P * rounds * ((double)ublocks * (K / s) + 0.25 * M);
+                    const double cost = P * rounds * ((double)ublocks * (K / s) + unit_cost * M);
                     if (cost < best - 1e-9) {
                         best = cost;
                         ps = s;

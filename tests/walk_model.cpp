@@ -65,6 +65,7 @@ std::string describe(const Case& c) {
 struct Launch {
     uint32_t per_cu;
     bool quad, allow_two, gulp;
+    double unit_cost;
     size_t fixed;
 };
 
@@ -75,6 +76,7 @@ Launch launch_of(Kind k, uint32_t M) {
     l.per_cu = dec ? kDecodePerCu : l.gulp ? gulp_per_cu((int)M) : kSipPerCu;
     l.quad = dec ? false : l.gulp ? gulp_quad((int)M) : sip_quad((int)M);
     l.allow_two = !l.gulp;
+    l.unit_cost = unit_end_cost(l.gulp, (int)M, dec);
     l.fixed = l.gulp ? kGulpStaticLds : kSipStaticLds;
     return l;
 }
@@ -201,7 +203,7 @@ void run(const Case& cs) {
     uint32_t grid = 0;
     size_t lds = 0;
     bool two = false;
-    if (!plan_launch(sh, row0, n, min_rows, M, kPlanWaves, l.per_cu, l.quad, l.fixed, l.allow_two, cs.cus, grid,
+    if (!plan_launch(sh, row0, n, min_rows, M, kPlanWaves, l.per_cu, l.quad, l.unit_cost, l.fixed, l.allow_two, cs.cus, grid,
                      lds, two))
         return;  // the generic kernel runs
     const bool dec = cs.kind == kDecodeSip || cs.kind == kDecodeGulp;
