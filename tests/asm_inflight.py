@@ -175,7 +175,7 @@ def kernels(asm: str, pattern: str):
 
 
 def metadata(asm: str) -> dict:
-    """-> {kernel name: {vgpr_count, sgpr_count, vgpr_spill_count,
+    """-> {kernel name: {vgpr_count, sgpr_count, agpr_count, vgpr_spill_count,
     sgpr_spill_count, private_segment_fixed_size, group_segment_fixed_size}}
     from the code object's metadata block of an assembly file (one entry of
     its kernel list per kernel, the keys in any order)."""
@@ -186,7 +186,7 @@ def metadata(asm: str) -> dict:
         if not name:
             continue
         fields = {}
-        for key in ("vgpr_count", "sgpr_count", "vgpr_spill_count", "sgpr_spill_count",
+        for key in ("vgpr_count", "sgpr_count", "agpr_count", "vgpr_spill_count", "sgpr_spill_count",
                     "private_segment_fixed_size", "group_segment_fixed_size"):
             mm = re.search(r"(?:^|\s)\.?" + key + r":\s+(\d+)", entry)
             if mm:

@@ -212,8 +212,8 @@ def test_no_scratch_and_no_vgpr_spill_in_kernels_with_untracked_loads(kernel_asm
     wait would move registers the compiler thinks are ready; SGPR spills go
     to lanes of VGPRs (v_writelane / v_readlane), which the in-flight walk
     above watches like any other register write or read. So: no scratch
-    instruction and no VGPR spill in any of these kernels; SGPR spills are
-    counted and reported."""
+    instruction, no VGPR spill and no AGPR in any of these kernels; SGPR
+    spills are counted and reported."""
     from tests.asm_inflight import metadata
 
     ks = kernels(kernel_asm, r"k_gemv_(sip|gulp)I")
@@ -223,6 +223,10 @@ def test_no_scratch_and_no_vgpr_spill_in_kernels_with_untracked_loads(kernel_asm
         assert name in md, f"{name}: no metadata"
         assert md[name].get("vgpr_spill_count", 0) == 0, f"{name}: {md[name]['vgpr_spill_count']} VGPR spills"
         assert "scratch_" not in body, f"{name}: scratch access"
+        # the in-flight walk tracks VGPRs and SGPRs: a kernel that used AGPRs (as spill space, or an
+        # MFMA's accumulators) would need the walk extended first
+        assert md[name].get("agpr_count", 0) == 0 and not re.search(r"v_accvgpr|\ba\[?\d", body), \
+            f"{name}: AGPRs in use"
         sgpr_spills[name] = md[name].get("sgpr_spill_count", 0)
         assert body.count("v_writelane_b32") >= sgpr_spills[name] > 0 or sgpr_spills[name] == 0
     print("SGPR spills (to VGPR lanes):", {k[20:60]: v for k, v in sgpr_spills.items() if v})
