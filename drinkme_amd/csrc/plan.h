@@ -507,8 +507,13 @@ inline bool plan_launch(SipShape& sh, const uint32_t* row0, uint32_t n, uint32_t
                 sh.ds = rem - sh.dr * ps;
                 sh.tbl2_lds = two ? (uint32_t)head : 0u;
                 // the dispatcher gives each CU one of the first cus
-                // workgroups, then a second from the rest
-                sh.young_from = per_cu == 2 ? cus : ~0u;
+                // workgroups, then a second from the rest; past 2 cus (a
+                // tile height that divides the group's boundaries) the
+                // later workgroups are no CU's second, only a later round,
+                // and the raised priority would take issue slots from the
+                // running ones (Qwen3-8B q/k/v at M = 4 7% slower with it,
+                // the 32B-class 26%), so no workgroup gets it
+                sh.young_from = per_cu == 2 && grid <= 2 * cus ? cus : ~0u;
                 grid_out = grid;
                 lds_out = lds;
                 two_out = two;
