@@ -16,9 +16,9 @@
 //                     raw twin (a raw bf16 weight through the same plan and
 //                     sums, radix_kernel_gpu.py:639-668) and the decode
 //                     (each block's bits stored instead of the products)
-//   k_gemv_gulp       the same for gulp (2, 2, 4, 8) streams (the schedule's
-//                     stream lengths, radix_kernel_gpu.py:292-392); M = 8 in
-//                     quad units; a decode mode
+//   k_gemv_gulp       the same for gulp (2, 2, 4, 8) streams
+//                     (radix_kernel_gpu.py:292-392); M = 8 in quad units; a
+//                     decode mode
 //   k_gemv_narrow     a raw row-major bf16 weight against M <= 8 rows
 //                     (radix_ops.gemv_narrow, radix_ops.py:177-249)
 //
@@ -521,7 +521,6 @@ struct SipGroup {
     const uint32_t* data[kGroupMax];
     const uint32_t* offsets[kGroupMax];
     const uint32_t* palette[kGroupMax];
-    const uint16_t* schedule[kGroupMax];  // gulp: the per-block tier stream lengths
     const void* bias[kGroupMax];
     void* out[kGroupMax];
     uint32_t row0[kGroupMax + 1];  // row0[n] = the group's row count
@@ -1255,9 +1254,12 @@ void k_gemv_sip(const SipGroup g, const uint16_t* __restrict__ x, const SipShape
 // tier 0 (64 words of 2-bit codes: palette entries 0..2, code 3 escapes),
 // tier 1 (2-bit codes of the tier-0 escapes: entries 3..5), tier 2 (4-bit
 // codes of the tier-1 escapes: entries 6..20) and the terminal (the raw
-// exponents of the tier-2 escapes). The per-block schedule
-// (dmx_radix_prepare) gives tier 1's and tier 2's word counts, so every
-// stream's start is known when the block's loads are issued.
+// exponents of the tier-2 escapes). The streams after tier 0 are short
+// (about 24 words a block on normal weights, 28 on Student-t ones), so one
+// load of a word a lane brings all three in; their starts follow from the
+// block's own counts as the schedule defines them (tier 1 holds the n1
+// tier-0 escapes in ceil(n1 / 16) words, tier 2 the n2 tier-1 escapes in
+// ceil(n2 / 8)), so the kernel does not read the per-block schedule.
 //
 // The work split, load pipeline and products are the sip kernel's. Lane l
 // owns weights 16l .. 16l + 15; per group of four weights:
@@ -1284,8 +1286,8 @@ void k_gemv_sip(const SipGroup g, const uint16_t* __restrict__ x, const SipShape
 
 struct GulpStage {
     u32x4 lit;
-    uint32_t t0, t1, t2, term;
-    uint32_t lsched;  // the schedule entry | the block's length in words << 16
+    uint32_t t0, tail;
+    uint32_t len;  // the block's length in words
 };
 
 
@@ -1297,38 +1299,31 @@ __device__ __forceinline__ uint32_t oob_past(uint32_t off, uint32_t last) {
     return off | ((last - off) & 0x80000000u);
 }
 
-// The block's five loads through the workgroup's buffer resource (based at
-// its first block), untracked by the compiler as in sip_load; completed by
-// GULP_WAIT. Reads reach at most word 320 + 64 + 128 + 63 of the block,
-// inside block_word_bounds(1024)[1] = 768. Tier 1's and the terminal's 64
-// lanes reach far past their few words: their lanes past the block's last
-// word read 0 and fetch nothing (else they load the next block's first
-// words, which that block fetches again).
-__device__ __forceinline__ GulpStage gulp_load(i32x4 rsrc, uint32_t base, uint2 o, uint32_t sched,
-                                               const GulpLanes& ln) {
+// The block's three loads through the workgroup's buffer resource (based
+// at its first block), untracked by the compiler as in sip_load; completed
+// by GULP_WAIT: the literal plane, the tier-0 words and the tail, words
+// 320 + lane, which hold tier 1, tier 2 and the terminal back to back
+// (their lengths follow from the block's own escape counts; blocks whose
+// tail is longer than 64 words take the exact path). Reads reach at most
+// word 383 of the block, inside block_word_bounds(1024)[1] = 768. The tail's
+// lanes past the block's last word read 0 and fetch nothing (else they load
+// the next block's first words, which that block fetches again).
+__device__ __forceinline__ GulpStage gulp_load(i32x4 rsrc, uint32_t base, uint2 o, const GulpLanes& ln) {
     GulpStage s;
-    s.lsched = (sched & 0xFFFFu) | ((o.y - o.x) << 16);
-    // (a schedule byte past its stream's widest keeps every read in the pad)
-    const uint32_t w1 = min(sched & 0xFFu, kGulpT1Max), w2 = min((sched >> 8) & 0xFFu, kGulpT2Max);
+    s.len = o.y - o.x;
     const uint32_t soff = (o.x - base) * 4u;
-    const uint32_t soff2 = soff + 4u * (kGulpFixed + w1);
-    // (the masked offsets ride in their loads' destinations)
-    const uint32_t last = 4u * (o.y - o.x) - 1u;
-    s.term = oob_past(ln.w + 4u * (kGulpFixed + w1 + w2), last);
-    s.t1 = oob_past(ln.w, last - 4u * kGulpFixed);  // (read at offset:1280, word 320)
+    // (the masked offset rides in its load's destination)
+    s.tail = oob_past(ln.w, 4u * (o.y - o.x) - 1u - 4u * kGulpFixed);  // (read at offset:1280, word 320)
     asm volatile(
-        "buffer_load_dword %0, %0, %5, %9 offen nt\n\t"
-        "buffer_load_dword %1, %6, %5, %8 offen nt\n\t"
-        "buffer_load_dword %2, %2, %5, %9 offen offset:1280 nt\n\t"
-        "buffer_load_dword %3, %10, %5, %9 offen offset:1024 nt\n\t"
-        "buffer_load_dwordx4 %4, %7, %5, %9 offen nt"
-        : "+&v"(s.term), "=&v"(s.t2), "+&v"(s.t1), "=&v"(s.t0), "=&v"(s.lit)
-        : "s"(rsrc), "v"(ln.t2), "v"(ln.lit), "s"(soff2), "s"(soff), "v"(ln.w));
+        "buffer_load_dword %0, %0, %3, %4 offen offset:1280 nt\n\t"
+        "buffer_load_dword %1, %5, %3, %4 offen offset:1024 nt\n\t"
+        "buffer_load_dwordx4 %2, %6, %3, %4 offen nt"
+        : "+&v"(s.tail), "=&v"(s.t0), "=&v"(s.lit)
+        : "s"(rsrc), "s"(soff), "v"(ln.w), "v"(ln.lit));
     return s;
 }
 
-#define GULP_WAIT(N, S) \
-    asm volatile("s_waitcnt vmcnt(" #N ")" : "+v"(S.lit), "+v"(S.t0), "+v"(S.t1), "+v"(S.t2), "+v"(S.term))
+#define GULP_WAIT(N, S) asm volatile("s_waitcnt vmcnt(" #N ")" : "+v"(S.lit), "+v"(S.t0), "+v"(S.tail))
 
 // Field i of width w of the little-endian stream at p, through the vector
 // memory path (the lane-serial fallback).
@@ -1404,7 +1399,6 @@ void k_gemv_gulp(const SipGroup g, const uint16_t* __restrict__ x, const SipShap
     const uint32_t units = (QUAD ? (nrows + 3) / 4 : nrows) * sh.segs;
     const uint32_t* data = pick(g.data, ia);
     const uint32_t* offsets = pick(g.offsets, ia);
-    const uint32_t* sched = reinterpret_cast<const uint32_t*>(pick(g.schedule, ia));
     uint32_t* x2 = x2_all + wv * kGulpX2Words;
 
     // the activation rows (first column phase), as in the sip kernel
@@ -1422,44 +1416,34 @@ void k_gemv_gulp(const SipGroup g, const uint16_t* __restrict__ x, const SipShap
         sip_start<false>(sh, p, wv, wk, sp);
         c = p;
     }
-    uint32_t ns = 0;  // the schedule of the last next_offsets() block
     auto next_offsets = [&]() {
         const uint32_t blk = QUAD ? quad_issue<false>(sh, pq, sp, nrows).blk : sip_issue<false>(sh, p, sp).blk;
         const uint2 o = sip_offsets(offsets, blk);
-        ns = (*(const_u32_ptr)(reinterpret_cast<const char*>(sched) + ((blk * 2u) & ~3u)) >> ((blk & 1u) * 16)) &
-             0xFFFFu;
         if constexpr (QUAD)
             quad_next(sh, pq, wk);
         else
             sip_next<false>(sh, p, wk, sp);
         return o;
     };
-    // the first blocks' directory and schedule entries, then the payload
-    // window's base: all issued before any is waited on
+    // the first blocks' directory entries, then the payload window's base:
+    // all issued before any is waited on
     const uint2 oA = next_offsets();
-    const uint32_t nA = ns;
     const uint2 oB = next_offsets();
-    const uint32_t nB = ns;
     uint2 oC = next_offsets();
-    uint32_t nC = ns;
     uint2 oD0 = make_uint2(0u, 0u);
-    uint32_t nD0 = 0;
-    if constexpr (QUAD) {
-        oD0 = next_offsets();
-        nD0 = ns;
-    }
+    if constexpr (QUAD) oD0 = next_offsets();
     const uint32_t base = ((const_u32_ptr)offsets)[sp.a_first];
     const i32x4 rsrc = make_rsrc(data + base, 0x7FFFFFFFu);
     const GulpLanes ln = gulp_lanes(lane);
-    GulpStage sA = gulp_load(rsrc, base, oA, nA, ln);
+    GulpStage sA = gulp_load(rsrc, base, oA, ln);
     __builtin_amdgcn_sched_barrier(0);
-    GulpStage sB = gulp_load(rsrc, base, oB, nB, ln);
+    GulpStage sB = gulp_load(rsrc, base, oB, ln);
     __builtin_amdgcn_sched_barrier(0);
     GulpStage sC, sD;
     if constexpr (QUAD) {  // (quad steps keep four blocks in flight: one step's)
-        sC = gulp_load(rsrc, base, oC, nC, ln);
+        sC = gulp_load(rsrc, base, oC, ln);
         __builtin_amdgcn_sched_barrier(0);
-        sD = gulp_load(rsrc, base, oD0, nD0, ln);
+        sD = gulp_load(rsrc, base, oD0, ln);
         __builtin_amdgcn_sched_barrier(0);
     }
 
@@ -1471,11 +1455,11 @@ void k_gemv_gulp(const SipGroup g, const uint16_t* __restrict__ x, const SipShap
         sel2[i] = make_uint2(b[0] | 0x0C00u | (b[1] << 16) | 0x0C000000u, b[2] | 0x0C00u | (b[3] << 16) | 0x0C000000u);
     }
     // the activation's direct loads precede the stages' loads (two stages:
-    // 10; quad mode four: 20)
+    // 6; quad mode four: 12)
     if constexpr (QUAD)
-        asm volatile("s_waitcnt vmcnt(20)" ::: "memory");
+        asm volatile("s_waitcnt vmcnt(12)" ::: "memory");
     else
-        asm volatile("s_waitcnt vmcnt(10)" ::: "memory");
+        asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
     __syncthreads();
 
     const uint32_t keep = 0x807F807Fu;
@@ -1514,21 +1498,13 @@ void k_gemv_gulp(const SipGroup g, const uint16_t* __restrict__ x, const SipShap
     auto process = [&](const GulpStage& s0, uint32_t* hout) {
         if (PH && !QUAD)
             while (cur_phase < c.p) phase_advance();
-        const uint32_t w1 = min(s0.lsched & 0xFFu, kGulpT1Max), w2 = min((s0.lsched >> 8) & 0xFFu, kGulpT2Max);
-        const uint32_t len = s0.lsched >> 16;
-        const bool has_term = len > kGulpFixed + w1 + w2;
+        const uint32_t len = s0.len;
         // tier 0
         const uint32_t T0 = s0.t0;
         const uint4 F0 = t0tab[T0 & 0xFF], F1 = t0tab[(T0 >> 8) & 0xFF], F2 = t0tab[(T0 >> 16) & 0xFF],
                     F3 = t0tab[T0 >> 24];
         uint2 E0 = make_uint2(F0.x, F0.y), E1 = make_uint2(F1.x, F1.y), E2 = make_uint2(F2.x, F2.y),
               E3 = make_uint2(F3.x, F3.y);
-        // lane j's two tier-2 codes (tier-1 escapes 2j, 2j + 1, in tier-2
-        // word j / 4, the one it loaded) and their palette bytes: read now,
-        // beside the tier-0 lookups
-        const uint32_t sh2 = (lane & 3u) << 3;
-        const uint32_t ca = (s0.t2 >> sh2) & 15u, cb = (s0.t2 >> (sh2 + 4)) & 15u;
-        const uint32_t pa = pal2[ca], pb = pal2[cb];
         // (M = 1 reads its activations late, beside the last lookups: the
         // registers stay free through the tier passes)
         const uint16_t* xb = xs + c.cb * 1024 + 8 * lane;
@@ -1536,23 +1512,19 @@ void k_gemv_gulp(const SipGroup g, const uint16_t* __restrict__ x, const SipShap
         // twice the tier-0 escapes of each group, and their prefix in the lane
         const uint32_t o1 = F0.z, o2 = o1 + F1.z, o3 = o2 + F2.z, cnt1 = (o3 + F3.z) >> 1;
         const uint32_t q0 = wave_scan_incl_dpp(cnt1) - cnt1;
+        // the tail (lane j holds its word j): tier 1 from word 0, w1 words
+        // for the block's n1 tier-0 escapes; tier 2 from word w1
+        const uint32_t w1 = (__builtin_amdgcn_readlane(q0 + cnt1, 63) + 15u) >> 4;
         // tier 1: the lane's codes, 2 bits each from bit 2 q0 of the stream
         const int k1 = (int)((q0 >> 2) & ~3u);
-        uint32_t v0 = __builtin_amdgcn_ds_bpermute(k1, s0.t1);
-        uint32_t v1 = __builtin_amdgcn_ds_bpermute(k1 + 4, s0.t1);
-        if (kGulpFixed + (__builtin_amdgcn_readlane(q0 + cnt1, 63) + 15u) / 16u > len) {
-            // a tier-1 stream past the block's end (a malformed block the
-            // gate passes) loaded zeros there: its words from memory, as a
-            // reader without an end bound takes them (the wait also
-            // completes the stages in flight)
-            const uint32_t soff1 = (block_start() - base) * 4u + 4u * kGulpFixed;
-            asm volatile("buffer_load_dword %0, %2, %3, %4 offen\n\t"
-                         "buffer_load_dword %1, %2, %3, %4 offen offset:4\n\t"
-                         "s_waitcnt vmcnt(0)"
-                         : "=&v"(v0), "=&v"(v1)
-                         : "v"(k1), "s"(rsrc), "s"(soff1)
-                         : "memory");
-        }
+        const uint32_t v0 = __builtin_amdgcn_ds_bpermute(k1, s0.tail);
+        const uint32_t v1 = __builtin_amdgcn_ds_bpermute(k1 + 4, s0.tail);
+        // lane j's two tier-2 codes (tier-1 escapes 2j, 2j + 1, in tier-2
+        // word j / 4) and their palette bytes: read beside tier 1's window
+        const uint32_t t2w = __builtin_amdgcn_ds_bpermute((int)(ln.t2 + 4u * w1), s0.tail);
+        const uint32_t sh2 = (lane & 3u) << 3;
+        const uint32_t ca = (t2w >> sh2) & 15u, cb = (t2w >> (sh2 + 4)) & 15u;
+        const uint32_t pa = pal2[ca], pb = pal2[cb];
         const uint32_t W1 = __builtin_amdgcn_alignbit(v1, v0, (q0 & 15u) << 1);
         // (the group's 2 popcount(m0) code bits from bit off, at byte
         // offset 8 t1_base(m0) + 8 codes)
@@ -1574,15 +1546,26 @@ void k_gemv_gulp(const SipGroup g, const uint16_t* __restrict__ x, const SipShap
         const uint32_t inc1 = wave_scan_incl(cnt2);
         const uint32_t q1 = inc1 - cnt2;
         const uint32_t n2 = __builtin_amdgcn_readlane(inc1, 63);
-        if (__builtin_expect(n2 > 128u || __builtin_amdgcn_ballot_w64(cnt2 > 8u) != 0, 0)) {
-            // exact lane-serial path over the streams in memory
+        const uint32_t w2 = (n2 + 7u) >> 3;  // tier 2's words, 4 bits a tier-1 escape
+        // The exact path takes a block with more tier-1 escapes than the
+        // exchange holds (128 a wave, 8 a lane), a tail past the one word
+        // each lane loaded, or streams past the block's end (a malformed
+        // block the gate passes, whose tail lanes there loaded zeros: the
+        // exact path reads memory, as a reader without an end bound does).
+        if (__builtin_expect(n2 > 128u || __builtin_amdgcn_ballot_w64(cnt2 > 8u) != 0 || len > kGulpFixed + 64u ||
+                                 kGulpFixed + w1 + w2 > len,
+                             0)) {
+            // exact lane-serial path over the streams in memory (tier 2's
+            // length recounted there: the tail's tier-1 words may be short)
             const uint32_t* tp = data + block_start();
             const uint32_t* s1 = tp + kGulpFixed;
             const uint32_t* s2 = s1 + w1;
-            const uint32_t* s3 = s2 + w2;
             uint32_t c2 = 0;
             for (uint32_t r = q0; r < q0 + cnt1; ++r) c2 += gulp_field(s1, r, 2) == 3u;
-            const uint32_t b1 = wave_scan_incl(c2) - c2;
+            const uint32_t i2 = wave_scan_incl(c2), b1 = i2 - c2;
+            const uint32_t w2x = (__builtin_amdgcn_readlane(i2, 63) + 7u) >> 3;
+            const uint32_t* s3 = s2 + w2x;
+            const bool has_term = len > kGulpFixed + w1 + w2x;
             uint32_t c3 = 0;
             for (uint32_t r = b1; r < b1 + c2; ++r) c3 += gulp_field(s2, r, 4) == 15u;
             const uint32_t b2 = wave_scan_incl(c3) - c3;
@@ -1630,6 +1613,7 @@ void k_gemv_gulp(const SipGroup g, const uint16_t* __restrict__ x, const SipShap
             uint32_t ea = pa, eb = pb;
             // (has_term, uniform and false unless the block has a terminal
             // stream, is tested first: then the per-lane tests are skipped)
+            const bool has_term = len > kGulpFixed + w1 + w2;
             bool ta = false, tb = false;
             if (has_term) {
                 ta = 2 * lane < n2 && ca == 15u;
@@ -1638,10 +1622,12 @@ void k_gemv_gulp(const SipGroup g, const uint16_t* __restrict__ x, const SipShap
             if (has_term && __builtin_amdgcn_ballot_w64(ta || tb) != 0) {
                 const uint32_t nt = (uint32_t)ta + (uint32_t)tb;
                 const uint32_t inc3 = wave_scan_incl(nt), q3 = inc3 - nt;
-                // terminal byte r is byte r & 3 of word r >> 2, held by lane r >> 2
+                // terminal byte r is byte r & 3 of its word r >> 2, tail word
+                // w1 + w2 + (r >> 2)
                 const uint32_t a3 = (q3 >> 2) << 2;
-                uint32_t u0 = __builtin_amdgcn_ds_bpermute((int)a3, s0.term);
-                uint32_t u1 = __builtin_amdgcn_ds_bpermute((int)a3 + 4, s0.term);
+                const int at = (int)(a3 + 4u * (w1 + w2));
+                uint32_t u0 = __builtin_amdgcn_ds_bpermute(at, s0.tail);
+                uint32_t u1 = __builtin_amdgcn_ds_bpermute(at + 4, s0.tail);
                 const uint32_t tstart = kGulpFixed + w1 + w2;
                 if (__builtin_amdgcn_readlane(inc3, 63) > 4u * (len - tstart)) {
                     // a terminal shorter than its escapes (a malformed block
@@ -1779,26 +1765,26 @@ void k_gemv_gulp(const SipGroup g, const uint16_t* __restrict__ x, const SipShap
             const uint32_t st_cb = cq.sp * sh.seg_blocks + cq.c, st_p = cq.p, st_row = 4 * cq.q;
             const uint32_t st_slot = st_row * sh.segs + cq.p * sh.psegs + cq.sp;
             const bool st_last = cq.c + 1 == sh.seg_blocks;
-            GULP_WAIT(15, sA);
+            GULP_WAIT(9, sA);
             process(sA, hq[0]);
             settle(hq[0]);
             uint2 oN = next_offsets();
-            sA = gulp_load(rsrc, base, oN, ns, ln);
-            GULP_WAIT(15, sB);
+            sA = gulp_load(rsrc, base, oN, ln);
+            GULP_WAIT(9, sB);
             process(sB, hq[1]);
             settle(hq[1]);
             oN = next_offsets();
-            sB = gulp_load(rsrc, base, oN, ns, ln);
-            GULP_WAIT(15, sC);
+            sB = gulp_load(rsrc, base, oN, ln);
+            GULP_WAIT(9, sC);
             process(sC, hq[2]);
             settle(hq[2]);
             oN = next_offsets();
-            sC = gulp_load(rsrc, base, oN, ns, ln);
-            GULP_WAIT(15, sD);
+            sC = gulp_load(rsrc, base, oN, ln);
+            GULP_WAIT(9, sD);
             process(sD, hq[3]);
             settle(hq[3]);
             oN = next_offsets();
-            sD = gulp_load(rsrc, base, oN, ns, ln);
+            sD = gulp_load(rsrc, base, oN, ln);
             if (PH)
                 while (cur_phase < st_p) phase_advance();
             quad_transpose(hq, lane);
@@ -1826,23 +1812,20 @@ void k_gemv_gulp(const SipGroup g, const uint16_t* __restrict__ x, const SipShap
             __builtin_amdgcn_s_setprio(0);
             young = false;
         }
-        sC = gulp_load(rsrc, base, oC, nC, ln);
+        sC = gulp_load(rsrc, base, oC, ln);
         uint2 oN = next_offsets();
-        uint32_t nN = ns;
-        GULP_WAIT(10, sA);
+        GULP_WAIT(6, sA);
         process(sA, nullptr);
-        sA = gulp_load(rsrc, base, oN, nN, ln);
+        sA = gulp_load(rsrc, base, oN, ln);
         oN = next_offsets();
-        nN = ns;
-        GULP_WAIT(10, sB);
+        GULP_WAIT(6, sB);
         process(sB, nullptr);
-        sB = gulp_load(rsrc, base, oN, nN, ln);
+        sB = gulp_load(rsrc, base, oN, ln);
         oC = next_offsets();
-        nC = ns;
-        GULP_WAIT(10, sC);
+        GULP_WAIT(6, sC);
         process(sC, nullptr);
     }
-    GULP_WAIT(5, sA);
+    GULP_WAIT(3, sA);
     if (k < items) process(sA, nullptr);
     GULP_WAIT(0, sB);
     if (k + 1 < items) process(sB, nullptr);
@@ -2108,7 +2091,6 @@ int launch_sip(const dmx_radix_tensor* const* ts, uint32_t n, const void* x, uin
         g.data[i] = t->data;
         g.offsets[i] = t->offsets;
         g.palette[i] = t->palette;
-        g.schedule[i] = t->schedule;
         g.bias[i] = bias ? bias[i < n ? i : n - 1] : nullptr;
         g.out[i] = out[i < n ? i : n - 1];
         g.row0[i] = (uint32_t)total;
@@ -2152,8 +2134,7 @@ bool is_gulp(const dmx_radix_tensor* t) {
 
 bool gulp_eligible(const dmx_radix_tensor* t, const void* x, int x_dtype, uint32_t m) {
     return g_policy.load() == DMX_POLICY_AUTO && m >= 1 && m <= 8 && x_dtype == DMX_BF16 && is_gulp(t) &&
-           t->block_size == 1024 && t->cols % 1024 == 0 && t->schedule &&
-           (reinterpret_cast<uintptr_t>(t->schedule) & 3u) == 0 && (reinterpret_cast<uintptr_t>(x) & 15u) == 0;
+           t->block_size == 1024 && t->cols % 1024 == 0 && (reinterpret_cast<uintptr_t>(x) & 15u) == 0;
 }
 
 typedef void (*GulpKernel)(const SipGroup, const uint16_t*, const SipShape);
@@ -2184,7 +2165,6 @@ int launch_gulp(const dmx_radix_tensor* const* ts, uint32_t n, const void* x, ui
         g.data[i] = t->data;
         g.offsets[i] = t->offsets;
         g.palette[i] = t->palette;
-        g.schedule[i] = t->schedule;
         g.bias[i] = bias ? bias[i < n ? i : n - 1] : nullptr;
         g.out[i] = out[i < n ? i : n - 1];
         g.row0[i] = (uint32_t)total;
@@ -2293,7 +2273,7 @@ extern "C" int dmx_radix_set_policy(int policy) {
 // (or would need column phases); the generic decoder then runs.
 int launch_decode_fast(const dmx_radix_tensor* t, uint16_t* out, hipStream_t stream, char* err, size_t errn) {
     const bool sip = is_sip(t);
-    const bool gulp = is_gulp(t) && t->schedule && (reinterpret_cast<uintptr_t>(t->schedule) & 3u) == 0;
+    const bool gulp = is_gulp(t);
     if (g_policy.load() != DMX_POLICY_AUTO || !(sip || gulp) || t->block_size != 1024 || t->cols % 1024 != 0 ||
         (reinterpret_cast<uintptr_t>(out) & 15u) != 0 || !fast_directory(t))
         return 2;
@@ -2303,7 +2283,6 @@ int launch_decode_fast(const dmx_radix_tensor* t, uint16_t* out, hipStream_t str
         g.data[i] = t->data;
         g.offsets[i] = t->offsets;
         g.palette[i] = t->palette;
-        g.schedule[i] = t->schedule;
         g.bias[i] = nullptr;
         g.out[i] = out;
         g.row0[i] = i == 0 ? 0u : t->rows;
@@ -2466,7 +2445,6 @@ int launch_raw(const uint16_t* w, uint32_t rows, uint32_t cols, bool gulp, const
         g.data[i] = reinterpret_cast<const uint32_t*>(w);
         g.offsets[i] = nullptr;
         g.palette[i] = nullptr;
-        g.schedule[i] = nullptr;
         g.bias[i] = bias;
         g.out[i] = out;
         g.row0[i] = i == 0 ? 0u : rows;

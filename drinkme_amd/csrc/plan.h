@@ -389,11 +389,10 @@ DMX_HD SipLanes sip_lanes(uint32_t lane) {
 }
 constexpr uint32_t kSipLitBytes = 16, kSipT0Bytes = 8, kSipTermBytes = 4;
 
-// gulp: 16 literal bytes (lit); tier-0 word l and tier-1 word l (w, plus
-// the streams' constant starts 256 and 320 words); tier-2 word l / 4 (t2,
-// from the tier-2 start 320 + w1) and terminal word l (w, from the
-// terminal start 320 + w1 + w2), w1 <= 64 and w2 <= 128 the schedule's
-// tier lengths, clamped.
+// gulp: 16 literal bytes (lit); tier-0 word l and tail word l (w, plus
+// the constant starts 256 and 320 words; the tail holds tier 1, tier 2 and
+// the terminal back to back). t2: the byte address, among the tail's lanes,
+// of lane l's tier-2 word l / 4 (from the tier-2 start w1).
 struct GulpLanes {
     uint32_t lit, w, t2;
 };
@@ -405,7 +404,6 @@ DMX_HD GulpLanes gulp_lanes(uint32_t lane) {
     ln.t2 = 4 * (lane >> 2);
     return ln;
 }
-constexpr uint32_t kGulpT1Max = 64, kGulpT2Max = 128;  // the clamps of a schedule's tier lengths
 
 // ---- the plan (host)
 

@@ -275,10 +275,7 @@ def prepare_schedule(data, offsets, C: int, widths, B: int, nblocks: int) -> tor
     t.n_widths = len(widths)
     for i, w in enumerate(widths):
         t.widths[i] = w
-    # one spare entry when nblocks is odd: the kernels read the schedule in
-    # aligned 4-byte words
-    n = int(nblocks)
-    sched = torch.zeros(n + (n & 1), dtype=torch.uint16, device=data.device)[:n]
+    sched = torch.zeros(int(nblocks), dtype=torch.uint16, device=data.device)
     err = _native.error_buffer()
     st = _native.lib().dmx_radix_prepare(ct.byref(t), sched.data_ptr(), _stream(), err, len(err))
     _native.check(st, err, "dmx_radix_prepare")

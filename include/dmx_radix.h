@@ -58,10 +58,10 @@ typedef struct dmx_radix_tensor {
                                  zero-padded to whole words, tiers concatenated
                                  (src/drinkme/codec/radix_pack.py:333-350) */
     const uint16_t* schedule; /* rx_schedule: one u16 per block for > 2 tiers, else NULL
-                                 (dmx_radix_prepare writes it). The gulp kernel reads it
-                                 in aligned 4-byte words: 4-byte aligned, with room for
-                                 an even number of entries; without it gulp GEMVs run on
-                                 the generic kernel */
+                                 (dmx_radix_prepare writes it). Carried for drinkme's
+                                 layout; no kernel here reads it (the gulp kernel finds
+                                 its streams from each block's own counts), so it may be
+                                 NULL */
     uint64_t payload_words;   /* NW */
     uint64_t pad_words;       /* zero words after the payload */
     uint32_t rows;            /* R */
@@ -105,10 +105,8 @@ int dmx_radix_decode(const dmx_radix_tensor* t, uint16_t* out, void* stream, cha
 /* Replaces radix_ops.prepare_schedule (src/drinkme/codec/radix_ops.py:
  * 341-348), the _prepare_schedule kernel (radix_kernel_gpu.py:44-66):
  * per block, byte (level - 1) = the word length of nonterminal tier
- * `level`'s stream, level >= 1. schedule: device, one u16 per block,
- * 4-byte aligned; allocate an even number of entries (a spare u16 when the
- * block count is odd), because the gulp kernel reads it in aligned 4-byte
- * words. Refuses a two-tier tensor (sip has no schedule). */
+ * `level`'s stream, level >= 1. schedule: device, one u16 per block.
+ * Refuses a two-tier tensor (sip has no schedule). */
 int dmx_radix_prepare(const dmx_radix_tensor* t, uint16_t* schedule, void* stream, char* err, size_t errn);
 
 /* Replaces radix_ops.gemv_fused / gemv / gemv_mc (src/drinkme/codec/

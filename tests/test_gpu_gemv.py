@@ -220,7 +220,8 @@ def _gulp_bits(rng, kind, shape):
 @pytest.mark.parametrize("M", [1, 3, 8])
 def test_gulp_fast_path(cuda, kind, M):
     """The gulp kernel (M = 1..8) across tier-1, tier-2 and terminal escape
-    densities, against the float64 bound and the generic kernel."""
+    densities, against the float64 bound and the generic kernel; with and
+    without the schedule in the descriptor."""
     import torch
 
     from drinkme_amd import radix_ops, swap
@@ -236,6 +237,10 @@ def test_gulp_fast_path(cuda, kind, M):
     print(f"case gulp fast {kind} M={M}", flush=True)
     y = radix_ops.gemv_rows(rt, x, None, torch.float32).cpu().numpy()
     _check_bound(y, O.bf16_bits_to_f32(xb), bits, f"gulp {kind} M={M}")
+    # the kernel finds its streams from each block's counts, not the
+    # schedule: a descriptor without one runs the same kernel, bit for bit
+    bare = dict(rt, rx_schedule=torch.empty(0, dtype=torch.uint16, device=cuda))
+    assert np.array_equal(radix_ops.gemv_rows(bare, x, None, torch.float32).cpu().numpy(), y), "without schedule"
     bias = bf16_tensor(O.f32_to_bf16_bits(rng.standard_normal(shape[0]).astype(np.float32)), cuda)
     fused = radix_ops.gemv_rows(rt, x, bias, torch.bfloat16)
     assert torch.equal(fused, (torch.from_numpy(y).to(cuda) + bias.float()).to(torch.bfloat16))

@@ -4,8 +4,8 @@
 
 The kernels bounds-check no read (the reach pad is the contract, as in
 drinkme's src/drinkme/codec/radix_gpu.py:13-27); what keeps their directory
-and schedule reads inside the arrays, and every block summed once into the
-right partial, is the walk. The model plans every configuration's launches
+reads inside the array, and every block summed once into the right partial,
+is the walk. The model plans every configuration's launches
 (the Qwen3-8B and 32B-class groups, lm_head, small and ragged groups, six
 hundred seeded random groups) for the sip, gulp, decode and raw-twin kernels
 at M = 1..8 and three CU counts, and walks every wave of every workgroup,

@@ -7,8 +7,7 @@
 // issuing as many loads past each wave's work as a pipeline may run ahead.
 // It checks, for every issue:
 //   - the directory index (offsets[blk] and offsets[blk + 1]) lies inside
-//     the tensor's R * NB + 1 entries, and (gulp) the aligned schedule word
-//     blk / 2 inside the schedule rounded up to whole words;
+//     the tensor's R * NB + 1 entries;
 //   - an issue on the wave's work is live and names the block the cursor
 //     claims: its row partial (slot), its column block among the resident
 //     activations, its column phase and whether it closes its unit; an issue
@@ -84,8 +83,7 @@ Launch launch_of(Kind k, uint32_t M) {
 // One launch: plan, walk, check. Returns false when no plan fits (the host
 // then runs the generic kernel, which has no cursor).
 template <bool TWO>
-void walk_launch(const Case& cs, const SipShape& sh, const uint32_t (&row0)[kGroupMax + 1], uint32_t grid,
-                 bool gulp) {
+void walk_launch(const Case& cs, const SipShape& sh, const uint32_t (&row0)[kGroupMax + 1], uint32_t grid) {
     const uint32_t W = sh.waves;
     std::vector<uint8_t> seen((size_t)sh.rows * sh.nb, 0);
     const std::string tag = describe(cs);
@@ -138,7 +136,6 @@ void walk_launch(const Case& cs, const SipShape& sh, const uint32_t (&row0)[kGro
                 if (is.blk >= tblocks)
                     bad(tag + ": directory index " + std::to_string(is.blk) + " past " + std::to_string(tblocks) +
                         " blocks (wg " + std::to_string(wg) + " wave " + std::to_string(wv) + ")");
-                if (gulp && (is.blk >> 1) >= (tblocks + 1) / 2) bad(tag + ": schedule word past the schedule");
                 const uint32_t grow = row0[tt] + is.blk / sh.nb, cbg = is.blk % sh.nb;
                 const uint32_t r = grow - wp.r0;  // the block's place in the tile, from its directory index
                 if (k < items && quad_live_row && !is.live) {
@@ -216,9 +213,9 @@ void run(const Case& cs) {
     if ((cs.kind == kTwinSip || cs.kind == kTwinGulp) && (uint64_t)sh.rows_per_wg * cs.cols * 2 >= (1ull << 31))
         return;  // the host refuses the fast twin
     if (two)
-        walk_launch<true>(cs, sh, row0, grid, l.gulp);
+        walk_launch<true>(cs, sh, row0, grid);
     else
-        walk_launch<false>(cs, sh, row0, grid, l.gulp);
+        walk_launch<false>(cs, sh, row0, grid);
 }
 
 // The per-lane loads against the reach pad (block_word_bounds(1024)[1]):
@@ -229,9 +226,8 @@ void check_reach() {
         const SipLanes s = sip_lanes(lane);
         sip_end = std::max({sip_end, s.lit + kSipLitBytes, s.t0 + kSipT0Bytes, s.term + kSipTermBytes});
         const GulpLanes g = gulp_lanes(lane);
-        const uint32_t t2s = 4 * (kGulpFixed + kGulpT1Max), ts = t2s + 4 * kGulpT2Max;
-        gulp_end = std::max({gulp_end, g.lit + 16, 4 * 256 + g.w + 4, 4 * kGulpFixed + g.w + 4, t2s + g.t2 + 4,
-                             ts + g.w + 4});
+        // literal plane, tier-0 word, tail word (tier 1, tier 2, terminal)
+        gulp_end = std::max({gulp_end, g.lit + 16, 4 * 256 + g.w + 4, 4 * kGulpFixed + g.w + 4});
     }
     if (sip_end > 4 * 608 || gulp_end > 4 * 768) bad("a lane's load reaches past the pad");
     printf("reach: sip loads end %u words past a block's start (pad 608), gulp %u (pad 768)\n", sip_end / 4,
