@@ -61,7 +61,8 @@ def test_fast_decode_of_whole_block_tensors(cuda, profile):
     """Whole-block sip and gulp tensors decode on their GEMV kernel's work
     split (decode mode): every bf16 pattern laid out in whole blocks, and
     escape-heavy tensors (the terminal path, and for sip a terminal longer
-    than 64 words), each equal to the source and to the generic decoder."""
+    than 64 words; for gulp, tails longer than 64 words), each equal to the
+    source and to the generic decoder."""
     from drinkme_amd import radix_ops, swap
 
     rng = np.random.default_rng(5 + len(profile))
@@ -69,6 +70,12 @@ def test_fast_decode_of_whole_block_tensors(cuda, profile):
              "escapes 3%": escape_heavy_bits(rng, (300, 4096), 0.03),
              "escapes 45%": escape_heavy_bits(rng, (64, 4096), 0.45),
              "tall": finite_bits(rng, (2050, 2048), spread=True)}
+    if profile == "gulp":
+        # blocks whose tier-1, tier-2 and terminal words run past the one
+        # word a lane loads (the exact path by the tail's length alone)
+        from tests.test_gpu_gemv import _gulp_bits
+
+        cases["long tail"] = _gulp_bits(rng, "long-tail", (300, 3072))
     for name, bits in cases.items():
         if O.pack(bits, profile).raw:
             continue

@@ -194,7 +194,24 @@ def _gulp_bits(rng, kind, shape):
         return synth.weight("gulp-test", 0, "t4", R, C, synth.STUDENT_T4)
     if kind == "spread":
         return finite_bits(rng, shape, spread=True)
-    if kind == "dense-tier1":
+    if kind == "long-tail":
+        # the ordinary rows set the palette (90% on three exponents, 6% on
+        # three more, 4% over 15 rare ones); every third row's blocks hold
+        # 68% tier-1 exponents and 1% past the palette: tails (tier 1, tier 2
+        # and the terminal) of 65-75 words, past the one word a lane loads,
+        # most with at most 128 tier-1 escapes (so only the tail's length
+        # sends them down the exact path)
+        u = rng.random(shape)
+        exps = np.where(u < 0.9, rng.integers(120, 123, size=shape),
+                        np.where(u < 0.96, rng.integers(116, 119, size=shape), rng.integers(60, 75, size=shape)))
+        rows = np.arange(R) % 3 == 0
+        v = rng.random((int(rows.sum()), C))
+        exps[rows] = np.where(v < 0.2, rng.integers(120, 123, size=v.shape),
+                              np.where(v < 0.88, rng.integers(116, 119, size=v.shape),
+                                       np.where(v < 0.99, rng.integers(60, 75, size=v.shape),
+                                                rng.integers(20, 40, size=v.shape))))
+        exps = exps.astype(np.uint16)
+    elif kind == "dense-tier1":
         # 12 equally likely exponents: half the weights escape tier 1 (more
         # than 128 per block: the lane-serial path)
         exps = rng.integers(100, 112, size=shape).astype(np.uint16)
@@ -216,7 +233,7 @@ def _gulp_bits(rng, kind, shape):
     return bits | (rng.integers(0, 2, shape, dtype=np.uint16) << 15)
 
 
-@pytest.mark.parametrize("kind", ["normal", "t4", "spread", "terminal", "dense-tier1", "terminal-heavy"])
+@pytest.mark.parametrize("kind", ["normal", "t4", "spread", "terminal", "dense-tier1", "terminal-heavy", "long-tail"])
 @pytest.mark.parametrize("M", [1, 3, 8])
 def test_gulp_fast_path(cuda, kind, M):
     """The gulp kernel (M = 1..8) across tier-1, tier-2 and terminal escape
@@ -229,8 +246,12 @@ def test_gulp_fast_path(cuda, kind, M):
     rng = np.random.default_rng(zlib.crc32(repr((kind, M)).encode()))
     shape = (300, 3072)
     bits = _gulp_bits(rng, kind, shape)
-    if O.pack(bits, "gulp").raw:
+    pk = O.pack(bits, "gulp")
+    if pk.raw:
         pytest.skip("stored raw")
+    if kind == "long-tail":
+        tail = np.diff(pk.offsets.astype(np.int64)) - 320
+        assert ((tail > 64) & ((O.schedule(pk) >> 8) <= 16)).sum() > 100, "the case lost its long tails"
     rt = swap.to_device_radix(oracle_dict(bits, "gulp"), cuda)
     xb = O.f32_to_bf16_bits(rng.standard_normal((M, shape[1])).astype(np.float32))
     x = bf16_tensor(xb, cuda)
