@@ -1270,18 +1270,20 @@ void k_gemv_sip(const SipGroup g, const uint16_t* __restrict__ x, const SipShape
 //   tier 1  the lane's tier-1 codes are a 32-bit window of the tier-1
 //           stream at bit 2 q0 (q0: the wave's exclusive prefix of tier-0
 //           escape counts), pulled from the lanes holding it (lane j holds
-//           tier-1 word j); the group's entry in m0's run of the 625-entry
+//           tail word j, tier 1 starting at word 0); the group's entry in m0's run of the 625-entry
 //           tier-1 table, at its 2 popcount(m0) code bits, gives the tier-1
 //           exponents at the escaped positions and the tier-1 escape mask
 //           m1;
 //   tier 2  lane j resolves tier-1 escapes 2j and 2j + 1 of the block from
-//           the tier-2 word it loaded (and the terminal, for code 15) and
+//           tier-2 word j / 4 (tail word w1 + j / 4, pulled like tier 1's;
+//           and the terminal after tier 2, for code 15) and
 //           writes their exponent bytes to the wave's LDS array; each lane
 //           reads the 8-byte window of that array at its first rank q1 and
 //           places the bytes with the selector table, as sip places its
 //           terminal bytes.
 // A block with more than 128 tier-1 escapes, or a lane with more than 8,
-// takes an exact lane-serial path that reads the streams from memory.
+// or a tail longer than 64 words, or streams past its end, takes an exact
+// lane-serial path that reads the streams from memory.
 
 
 struct GulpStage {
