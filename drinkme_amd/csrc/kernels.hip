@@ -1554,9 +1554,10 @@ void k_gemv_gulp(const SipGroup g, const uint16_t* __restrict__ x, const SipShap
         // each lane loaded, or streams past the block's end (a malformed
         // block the gate passes, whose tail lanes there loaded zeros: the
         // exact path reads memory, as a reader without an end bound does).
-        if (__builtin_expect(n2 > 128u || __builtin_amdgcn_ballot_w64(cnt2 > 8u) != 0 || len > kGulpFixed + 64u ||
-                                 kGulpFixed + w1 + w2 > len,
-                             0)) {
+        // (the three uniform tests as one sign bit: every quantity here is
+        // far below 2^31, so a difference that goes negative sets bit 31)
+        const uint32_t past = (128u - n2) | (kGulpFixed + 64u - len) | (len - (kGulpFixed + w1 + w2));
+        if (__builtin_expect((int32_t)past < 0 || __builtin_amdgcn_ballot_w64(cnt2 > 8u) != 0, 0)) {
             // exact lane-serial path over the streams in memory (tier 2's
             // length recounted there: the tail's tier-1 words may be short)
             const uint32_t* tp = data + block_start();
