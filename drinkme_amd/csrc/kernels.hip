@@ -725,7 +725,7 @@ __device__ __forceinline__ void sip_table(uint2* tb, const uint32_t* palette) {
 constexpr int kModeGemv = 0, kModeTwinSip = 1, kModeTwinGulp = 2, kModeDecode = 3;
 
 template <bool TWO, int M, bool PH, int MODE = kModeGemv>
-__global__ __launch_bounds__(kSipThreads, (M == 8 || (M == 4 && (PH || (MODE == kModeTwinGulp ? gulp_quad(4) : sip_quad(4))))) ? 3 : 6)
+__global__ __launch_bounds__(kSipThreads, (M == 8 || (M == 4 && (MODE == kModeTwinGulp ? gulp_quad(4) : (PH || sip_quad(4))))) ? 3 : 6)
 void k_gemv_sip(const SipGroup g, const uint16_t* __restrict__ x, const SipShape sh) {
     constexpr bool RAW = MODE == kModeTwinSip || MODE == kModeTwinGulp, DEC = MODE == kModeDecode;
     // verify rows four output rows at a time on the matrix cores (a raw twin
@@ -1375,7 +1375,7 @@ __device__ __forceinline__ void gulp_tables(uint4* t0tab, uint2* t1tab, uint8_t*
 // DEC: decode only, each block's bf16 bits stored to the tensor's output
 // (row-major [rows, cols]) in place of the products.
 template <int M, bool PH, bool DEC = false>
-__global__ __launch_bounds__(kSipThreads, (M == 8 || (M == 4 && (PH || gulp_quad(4)))) ? 3 : 6)
+__global__ __launch_bounds__(kSipThreads, (M == 8 || (M == 4 && gulp_quad(4))) ? 3 : 6)
 void k_gemv_gulp(const SipGroup g, const uint16_t* __restrict__ x, const SipShape sh) {
     static_assert(!DEC || (M == 1 && !PH), "the decode runs unphased");
     constexpr int W = kSipWaves, TH = kSipThreads;

@@ -469,7 +469,17 @@ inline bool plan_launch(SipShape& sh, const uint32_t* row0, uint32_t n, uint32_t
         if (T <= min_rows && (allow_two || !two)) {
             for (uint32_t P = 1; P <= sh.nb; ++P) {
                 if (sh.nb % P) continue;
-                if (P > 1 && M >= 4 && per_cu > 1) break;  // (phased kernels at M >= 4: one workgroup per CU)
+                if (P > 1 && M >= 4 && per_cu > 1) {
+                    // phased kernels at M >= 4 keep one workgroup per CU
+                    // (quad and M = 8: their registers), unless one per CU
+                    // would need phases too (gulp's v_dot2 rows: its
+                    // phased kernel fits six waves per SIMD, and two
+                    // workgroups per CU hide its decode better than one
+                    // without phases; where one fits unphased, the phase
+                    // barriers cost more than the second workgroup gains)
+                    const size_t unphased = 2 * (size_t)M * (sh.nb * 1024) + fixed;
+                    if (quad || M == 8 || unphased <= kLdsBytes) break;
+                }
                 const uint32_t K = sh.nb / P;
                 double best = 1e30;
                 uint32_t ps = 1;
