@@ -670,9 +670,10 @@ __device__ __forceinline__ void lds_load16(const void* g, uint32_t lds) {
         : "memory");
 }
 
-template <int M, int THREADS>
+// THREADS: the workgroup's threads (a wave-uniform value)
+template <int M>
 __device__ __forceinline__ void load_x_slice(const SipShape& sh, const uint16_t* __restrict__ x, uint16_t* xs,
-                                             uint32_t phase) {
+                                             uint32_t phase, uint32_t THREADS) {
     const uint32_t lane = lane_id(), wbase = wave_id() * 64u;
     const uint32_t row_chunks = sh.phase_blocks * 128u, xchunks = sh.cols / 8, first = phase * row_chunks;
     const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_ptr)xs;
@@ -764,7 +765,7 @@ void k_gemv_sip(const SipGroup g, const uint16_t* __restrict__ x, const SipShape
     // the activation (its first column phase) goes to LDS by direct loads
     // (no registers staged), first in the queue: small and hot in L2; the
     // barrier below waits for it
-    if constexpr (!DEC) load_x_slice<M, kSipThreads>(sh, x, xs, 0);
+    if constexpr (!DEC) load_x_slice<M>(sh, x, xs, 0, kSipThreads);
 
     // the first two blocks' loads go out before the tables are built; a
     // cursor past the wave's work reads the workgroup's first block instead
@@ -914,7 +915,7 @@ void k_gemv_sip(const SipGroup g, const uint16_t* __restrict__ x, const SipShape
     auto phase_advance = [&]() {
         __syncthreads();
         ++cur_phase;
-        load_x_slice<M, kSipThreads>(sh, x, xs, cur_phase);
+        load_x_slice<M>(sh, x, xs, cur_phase, kSipThreads);
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
     };
@@ -1352,11 +1353,13 @@ __device__ __forceinline__ uint32_t gulp_field(const uint32_t* p, uint32_t i, ui
 //       (1 + 4)^4 = 625 entries (a table indexed by m0 and four whole
 //       codes would hold 4096, mostly repeats).
 //   pal2[c]: tier 2's bytes.
-template <int THREADS>
-__device__ __forceinline__ void gulp_tables(uint4* t0tab, uint2* t1tab, uint8_t* pal2, const uint32_t* palette) {
+__device__ __forceinline__ void gulp_tables(uint4* t0tab, uint2* t1tab, uint8_t* pal2, const uint32_t* palette,
+                                            uint32_t THREADS) {
     const const_u32_ptr pw = (const_u32_ptr)palette;
     const uint32_t p0 = pw[0], p1 = pw[1];
-    for (uint32_t i = threadIdx.x; i < 256; i += THREADS) {
+    // (every plan's workgroup has at least 512 threads: one entry each)
+    if (threadIdx.x < 256) {
+        const uint32_t i = threadIdx.x;
         uint32_t f[4];
         gulp_t0_entry(p0, i, f);
         t0tab[i] = make_uint4(f[0], f[1], f[2], f[3]);
@@ -1374,18 +1377,20 @@ __device__ __forceinline__ void gulp_tables(uint4* t0tab, uint2* t1tab, uint8_t*
 
 // DEC: decode only, each block's bf16 bits stored to the tensor's output
 // (row-major [rows, cols]) in place of the products.
-template <int M, bool PH, bool DEC = false>
-__global__ __launch_bounds__(kSipThreads, (M == 8 || (M == 4 && gulp_quad(4))) ? 3 : 6)
+// WV: waves per workgroup, the plan's (12, or 8 at three workgroups per CU).
+template <int M, bool PH, bool DEC = false, int WV = kSipWaves>
+__global__ __launch_bounds__(WV * 64, (M == 8 || (M == 4 && gulp_quad(4))) ? 3 : 6)
 void k_gemv_gulp(const SipGroup g, const uint16_t* __restrict__ x, const SipShape sh) {
     static_assert(!DEC || (M == 1 && !PH), "the decode runs unphased");
-    constexpr int W = kSipWaves, TH = kSipThreads;
+    static_assert(WV == kSipWaves || (!PH && !DEC && !gulp_quad(M)), "8-wave workgroups run unphased v_dot2 rows");
+    constexpr uint32_t W = WV, TH = 64u * WV;
     // verify rows four output rows at a time on the matrix cores
     constexpr bool QUAD = !DEC && gulp_quad(M);
     __shared__ uint4 t0tab[256];
     __shared__ uint2 t1tab[kGulpT1Entries];
     __shared__ uint2 sel2[13 * 16];
     __shared__ uint32_t pal2w[4];
-    __shared__ uint32_t x2_all[W * kGulpX2Words];
+    __shared__ uint32_t x2_all[kSipWaves * kGulpX2Words];
     extern __shared__ __align__(16) uint8_t lds_dyn[];
     uint16_t* xs = reinterpret_cast<uint16_t*>(lds_dyn);
     // (a multiple of 8 bf16, stated so that 16-byte LDS reads of the rows stay whole)
@@ -1404,7 +1409,7 @@ void k_gemv_gulp(const SipGroup g, const uint16_t* __restrict__ x, const SipShap
     uint32_t* x2 = x2_all + wv * kGulpX2Words;
 
     // the activation rows (first column phase), as in the sip kernel
-    if constexpr (!DEC) load_x_slice<M, TH>(sh, x, xs, 0);
+    if constexpr (!DEC) load_x_slice<M>(sh, x, xs, 0, TH);
 
     // p issues the loads, c follows it over the blocks processed (quad mode:
     // pq and cq)
@@ -1449,9 +1454,9 @@ void k_gemv_gulp(const SipGroup g, const uint16_t* __restrict__ x, const SipShap
         __builtin_amdgcn_sched_barrier(0);
     }
 
-    gulp_tables<TH>(t0tab, t1tab, reinterpret_cast<uint8_t*>(pal2w), pick(g.palette, ia));
-    for (uint32_t i = threadIdx.x; i < 13 * 16; i += TH) {
-        const uint32_t m = i & 15, o = i >> 4;
+    gulp_tables(t0tab, t1tab, reinterpret_cast<uint8_t*>(pal2w), pick(g.palette, ia), TH);
+    if (threadIdx.x < 13 * 16) {  // (at least 512 threads)
+        const uint32_t i = threadIdx.x, m = i & 15, o = i >> 4;
         uint32_t b[4];
         for (uint32_t k = 0, r = o; k < 4; ++k) b[k] = (m >> k) & 1 ? (r++ & 7) : 0x0Cu;
         sel2[i] = make_uint2(b[0] | 0x0C00u | (b[1] << 16) | 0x0C000000u, b[2] | 0x0C00u | (b[3] << 16) | 0x0C000000u);
@@ -1483,7 +1488,7 @@ void k_gemv_gulp(const SipGroup g, const uint16_t* __restrict__ x, const SipShap
     auto phase_advance = [&]() {
         __syncthreads();
         ++cur_phase;
-        load_x_slice<M, TH>(sh, x, xs, cur_phase);
+        load_x_slice<M>(sh, x, xs, cur_phase, TH);
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
     };
@@ -2142,11 +2147,15 @@ bool gulp_eligible(const dmx_radix_tensor* t, const void* x, int x_dtype, uint32
 
 typedef void (*GulpKernel)(const SipGroup, const uint16_t*, const SipShape);
 
-GulpKernel gulp_kernel(bool phased, int mi) {
+// waves: the plan's waves per workgroup (8 only unphased, M <= 4)
+GulpKernel gulp_kernel(bool phased, int mi, uint32_t waves = kSipWaves) {
     static const GulpKernel table[2][4] = {
         {k_gemv_gulp<1, false>, k_gemv_gulp<2, false>, k_gemv_gulp<4, false>, k_gemv_gulp<8, false>},
         {k_gemv_gulp<1, true>, k_gemv_gulp<2, true>, k_gemv_gulp<4, true>, k_gemv_gulp<8, true>}};
-    return table[phased ? 1 : 0][mi];
+    static const GulpKernel table8[3] = {k_gemv_gulp<1, false, false, kGulpWaves3>,
+                                         k_gemv_gulp<2, false, false, kGulpWaves3>,
+                                         k_gemv_gulp<4, false, false, kGulpWaves3>};
+    return waves == kGulpWaves3 && !phased && mi < 3 ? table8[mi] : table[phased ? 1 : 0][mi];
 }
 
 // One launch of the gulp kernel over n tensors of equal cols (already
@@ -2190,17 +2199,16 @@ int launch_gulp(const dmx_radix_tensor* const* ts, uint32_t n, const void* x, ui
     uint32_t grid = 0;
     size_t lds = 0;
     bool two = false;
-    if (!plan_launch(sh, g.row0, n, min_rows, M, kSipWaves, gulp_per_cu((int)M), gulp_quad((int)M),
-                     unit_end_cost(true, (int)M, false), fixed, false,
-                     (uint32_t)cu_count(), grid, lds, two))
-        return 2;
+    if (!plan_gulp(sh, g.row0, n, min_rows, M, (uint32_t)cu_count(), grid, lds, two)) return 2;
     {
-        const void* kerns[8];
+        const void* kerns[11];
         for (int t = 0; t < 2; ++t)
             for (int i = 0; i < 4; ++i) kerns[4 * t + i] = reinterpret_cast<const void*>(gulp_kernel(t, i));
-        if (raise_lds_limit(kFamGulp, kerns, 8, lds, 64 * 1024 - fixed, "gulp kernel LDS opt-in", err, errn)) return 1;
+        for (int i = 0; i < 3; ++i) kerns[8 + i] = reinterpret_cast<const void*>(gulp_kernel(false, i, kGulpWaves3));
+        if (raise_lds_limit(kFamGulp, kerns, 11, lds, 64 * 1024 - fixed, "gulp kernel LDS opt-in", err, errn)) return 1;
     }
-    hipLaunchKernelGGL(gulp_kernel(sh.phases > 1, mi), dim3(grid), dim3(kSipThreads), lds, stream, g,
+    if (sh.waves != kSipWaves && (sh.waves != kGulpWaves3 || sh.phases > 1 || mi == 3)) return 2;
+    hipLaunchKernelGGL(gulp_kernel(sh.phases > 1, mi, sh.waves), dim3(grid), dim3(64u * sh.waves), lds, stream, g,
                        static_cast<const uint16_t*>(x), sh);
     return launch_check(err, errn, "gulp gemv launch");
 }

@@ -41,6 +41,8 @@ namespace dmx {
 
 constexpr int kGroupMax = 4;          // tensors per grouped launch
 constexpr uint32_t kPlanWaves = 12;   // waves per workgroup of the sip and gulp kernels
+constexpr uint32_t kGulpWaves3 = 8;   // gulp's waves per workgroup at three workgroups per CU
+static_assert(kGulpWaves3 * 64 >= 256 && kPlanWaves * 64 >= 256, "the gulp tables take one entry a thread");
 constexpr uint32_t kSipFixed = 256 + 96;   // sip: literal plane + tier-0 words of a 1024-weight block
 constexpr uint32_t kGulpFixed = 256 + 64;  // gulp: literal plane + tier-0 words
 constexpr uint32_t kTableBytes = 4096 * 8;  // one sip exponent table (a second one for a tile spanning two tensors)
@@ -531,6 +533,34 @@ inline bool plan_launch(SipShape& sh, const uint32_t* row0, uint32_t n, uint32_t
         if (per_cu == 1) break;
     }
     return false;
+}
+
+// gulp's launch plan. A group whose tensor boundaries the tiles must not
+// cut can take more tiles than two workgroups per CU hold: its later tiles
+// then run as another round, and tiles of few rows leave waves of a
+// 12-wave workgroup without a unit. Those launches (more than two tiles a
+// CU, at most three) run 8-wave workgroups, three per CU, all resident at
+// once.
+inline bool plan_gulp(SipShape& sh, const uint32_t* row0, uint32_t n, uint32_t min_rows, uint32_t M, uint32_t cus,
+                      uint32_t& grid_out, size_t& lds_out, bool& two_out) {
+    const double uc = unit_end_cost(true, (int)M, false);
+    if (!plan_launch(sh, row0, n, min_rows, M, kPlanWaves, gulp_per_cu((int)M), gulp_quad((int)M), uc, kGulpStaticLds,
+                     false, cus, grid_out, lds_out, two_out))
+        return false;
+    if (!gulp_quad((int)M) && grid_out > 2 * cus && grid_out <= 3 * cus) {
+        SipShape s3 = sh;
+        uint32_t g3 = 0;
+        size_t l3 = 0;
+        bool t3 = false;
+        if (plan_launch(s3, row0, n, min_rows, M, kGulpWaves3, 3, false, uc, kGulpStaticLds, false, cus, g3, l3, t3) &&
+            g3 <= 3 * cus && s3.phases == 1 && (l3 + kGulpStaticLds) * 3 <= kLdsBytes) {
+            sh = s3;
+            grid_out = g3;
+            lds_out = l3;
+            two_out = t3;
+        }
+    }
+    return true;
 }
 
 }  // namespace dmx

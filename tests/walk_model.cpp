@@ -200,8 +200,10 @@ void run(const Case& cs) {
     uint32_t grid = 0;
     size_t lds = 0;
     bool two = false;
-    if (!plan_launch(sh, row0, n, min_rows, M, kPlanWaves, l.per_cu, l.quad, l.unit_cost, l.fixed, l.allow_two, cs.cus, grid,
-                     lds, two))
+    // (the gulp GEMV plans through plan_gulp, as its launcher does)
+    if (cs.kind == kGulp ? !plan_gulp(sh, row0, n, min_rows, M, cs.cus, grid, lds, two)
+                         : !plan_launch(sh, row0, n, min_rows, M, kPlanWaves, l.per_cu, l.quad, l.unit_cost, l.fixed,
+                                        l.allow_two, cs.cus, grid, lds, two))
         return;  // the generic kernel runs
     const bool dec = cs.kind == kDecodeSip || cs.kind == kDecodeGulp;
     if (dec && sh.phases > 1) return;  // the decode runs unphased, else generic
