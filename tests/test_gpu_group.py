@@ -64,13 +64,15 @@ def test_group_matches_the_oracle(cuda, rows, C, M):
     assert all(torch.equal(a, b) for a, b in zip(again, ys))
 
 
-@pytest.mark.parametrize("rows,C,M", [((4096, 1024, 1024), 4096, 1), ((4096, 1024, 1024), 4096, 4),
+@pytest.mark.parametrize("rows,C,M", [((4096, 1024, 1024), 4096, 1), ((4096, 1024, 1024), 4096, 2),
+                                      ((4096, 1024, 1024), 4096, 4),
                                       ((8192, 1024, 1024), 5120, 1), ((12288, 12288), 4096, 1),
                                       ((640, 128, 128), 1024, 8), ((1000, 37, 2000), 2048, 1)])
 def test_gulp_group_matches_the_oracle(cuda, rows, C, M):
     """gulp groups: the kernel keeps one tensor per workgroup, so q/k/v-like
     groups run as one launch with a tile height that divides every tensor
-    boundary (8 rows for 4096/1024/1024); a group with no such height
+    boundary (8 rows for 4096/1024/1024: 768 tiles, so 8-wave workgroups,
+    three per CU, at M = 1, 2 and 4); a group with no such height
     (1000/37/2000) runs tensor by tensor. Same bars as sip."""
     import torch
 
