@@ -35,8 +35,9 @@ Reported:
   cpu_baseline  drinkme's CPU route on the host's cores: the compiled
               drinkme decoder (oracle/_ref) + torch F.linear, on a bounded
               sample (layer 0), scaled to the step by weight count; three
-              legs (all host threads, one thread, and F.linear over the
-              cached decoded weight), `value` the all-threads leg
+              legs (every thread of the job's CPU share, one thread, and
+              F.linear over the cached decoded weight), `value` the first;
+              nproc and the CPUs the process may run on are recorded
 One JSON line goes to stdout; progress lines go to stderr.
 """
 
@@ -53,6 +54,7 @@ sys.path.insert(0, ROOT)
 
 PEAK_GBPS = 8000.0  # MI355X HBM3E
 PALETTE_BYTES = {"sip": 7, "balanced": 10, "gulp": 21}
+CPU_SHARE = 16  # host threads the CPU legs use at most: one GPU's share of its host's cores
 
 
 def log(msg: str) -> None:
@@ -136,14 +138,36 @@ def time_graph(fn, replays: int, warmup: int, settle_s: float = 0.0, info: dict 
     return start.elapsed_time(end) / replays
 
 
+def time_eager(fn, reps: int, warmup: int) -> tuple:
+    """(milliseconds per call of `fn` on the GPU's clock, milliseconds the
+    host spent issuing one call): `fn` launched eagerly, no graph, HIP
+    events around `reps` calls after `warmup` untimed ones."""
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        fn()
+    host_ms = (time.perf_counter() - t0) * 1e3 / reps
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / reps, host_ms
+
+
 def cpu_baseline(tensors, xs, budget_s: float = 10.0):
     """drinkme's CPU route (src/drinkme/codec/swap.py:344-352): decode the
     weight with drinkme's compiled C++ decoder (oracle/_ref; the oracle's C
     decoder when that library is absent), then torch F.linear on the bf16
     weight. Three legs, each on a bounded sample of the workload and scaled
     to the whole sweep by weight count:
-      all_cores   decode on every host thread (up to 16, over row ranges) +
-                  F.linear on as many; per call (value is this leg's rate)
+      cpu_share   decode on every thread of the job's CPU share (the CPUs
+                  the process may run on, at most 16: a one-GPU job's share
+                  of its host) over row ranges + F.linear on as many; per
+                  call (value is this leg's rate)
       one_thread  decode and F.linear on one thread: the serve route's own
                   decode runs single-threaded (radix_native.py:221, called
                   without workers from radix_pack.py:292-294)
@@ -158,7 +182,9 @@ def cpu_baseline(tensors, xs, budget_s: float = 10.0):
     from oracle import radix_oracle as O
 
     kind = "reference" if O.ref_available() else "port"
-    threads = min(os.cpu_count() or 1, 16)
+    nproc = os.cpu_count() or 1
+    allowed = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else nproc
+    threads = max(1, min(allowed, CPU_SHARE))
     sample = [t for t in tensors if t["layer"] == tensors[0]["layer"]]
     host = []
     for t in sample:
@@ -211,7 +237,7 @@ def cpu_baseline(tensors, xs, budget_s: float = 10.0):
     legs = {}
     torch.set_num_threads(threads)
     per, reps, w = timed(lambda h: torch.nn.functional.linear(xcpu[h[4]], decode(h, threads)), host, budget_s)
-    legs["all_cores"] = leg("all_cores", per, w, reps, threads,
+    legs["cpu_share"] = leg("cpu_share", per, w, reps, threads,
                             f"decode (drinkme C++ decoder, {threads} threads over row ranges) + torch F.linear "
                             f"bf16 ({threads} threads) per call")
     torch.set_num_threads(1)
@@ -224,8 +250,10 @@ def cpu_baseline(tensors, xs, budget_s: float = 10.0):
                          [(W, C, 0, W.shape[0], W.shape[1]) for W, C in weights], 0.4 * budget_s)
     legs["cached_w"] = leg("cached_w", per, w, reps, threads,
                            f"torch F.linear bf16 ({threads} threads) over the decoded weight, kept between calls")
-    out = dict(legs["all_cores"])
-    out.update(kind=kind, legs=legs)
+    out = dict(legs["cpu_share"])
+    out.update(kind=kind, legs=legs, nproc=nproc, affinity_cpus=allowed,
+               threads_note=f"{threads} threads: the CPUs this process may run on ({allowed} of nproc {nproc}), "
+                            f"at most {CPU_SHARE}, the host CPUs a one-GPU job is given")
     return out
 
 
@@ -354,6 +382,20 @@ def main() -> int:
     ms_u = time_graph(sweep_ungrouped, args.steps, args.warmup)
     log(f"sweep ungrouped ({len(tensors)} launches): {ms_u * 1e3:.1f} us, "
         f"{total_bytes / (ms_u * 1e-3) / 1e9:.0f} GB/s compressed")
+    # drinkme's own launch pattern: one call per Linear through the radix_ops
+    # surface (gemv_fused at M = 1, the fused rows call above), eagerly on the
+    # current stream, each call allocating its output (swap.py:443-456)
+    def sweep_eager():
+        for t in tensors:
+            x = xs[t["C"]]
+            if args.m == 1:
+                radix_ops.gemv_fused(t["rt"], x[0], None, torch.bfloat16)
+            else:
+                radix_ops.gemv_rows(t["rt"], x, None, torch.bfloat16)
+
+    ms_e, host_e = time_eager(sweep_eager, args.steps, args.warmup)
+    log(f"sweep eager, one radix_ops call per Linear ({len(tensors)} launches): {ms_e * 1e3:.1f} us "
+        f"({host_e * 1e3:.0f} us of host issue), {total_bytes / (ms_e * 1e-3) / 1e9:.0f} GB/s compressed")
     traffic = None
     tf = os.path.join(ROOT, "profiles", "traffic.json")
     key = f"k_gemv_{args.profile} {dom_shape} {args.profile} M={args.m}"
@@ -390,6 +432,10 @@ def main() -> int:
             "launches": len(groups), "grouping": "q/k/v and gate/up of a layer share x: one launch each",
             "ungrouped": {"launches": len(tensors), "us_per_sweep": round(ms_u * 1e3, 2),
                           "value": round(total_bytes / (ms_u * 1e-3) / 1e9, 1)},
+            "eager_ungrouped": {"launches": len(tensors), "us_per_sweep": round(ms_e * 1e3, 2),
+                                "value": round(total_bytes / (ms_e * 1e-3) / 1e9, 1),
+                                "host_issue_us_per_sweep": round(host_e * 1e3, 1),
+                                "calls": "radix_ops.gemv_fused per Linear (gemv_rows at M > 1), eager, no graph"},
             "timing": "HIP graph of the sweep, replayed; events around the timed replays",
             "weights_rng": f"dmx_synth_bf16 seed {synth.SEED}, one stream per (workload, layer, tensor)",
         },

@@ -1761,8 +1761,8 @@ void k_gemv_gulp(const SipGroup g, const uint16_t* __restrict__ x, const SipShap
     const uint32_t items = my_units * sh.seg_blocks * (QUAD ? 4 : 1);
     if constexpr (QUAD) {
         // a quad step (as in the sip kernel): the four rows' blocks of one
-        // column block, stages A, B, C and D, each completed (15 loads newer:
-        // the other three stages), decoded and refilled at once with the
+        // column block, stages A, B, C and D, each completed (nine loads
+        // newer: the other three stages' three each), decoded and refilled at once with the
         // block four ahead; then the four rows meet the activation rows on
         // the matrix cores. One workgroup per CU (its registers), so no
         // workgroup priorities.

@@ -170,13 +170,19 @@ def to_device_twin(w_bf16, widths=(3, 8), device: str = "cuda") -> dict:
             "codec": "twin", "layout": 0}
 
 
+def _bits_as_bf16(bits, shape, device) -> torch.Tensor:
+    """u16 bit patterns -> a bf16 tensor of `shape` on `device` holding
+    exactly those bits (its own copy, never a view of the numpy array)."""
+    host = torch.from_numpy(np.ascontiguousarray(bits, dtype=np.uint16).view(np.int16)).view(torch.bfloat16)
+    return host.reshape(shape).to(torch.device(device), copy=True)
+
+
 def to_device_raw(pack: dict, device: str = "cuda") -> dict:
     """A tensor stored raw (radix would have expanded it: codec "raw", its
     bf16 bits as raw_bits) as its resident bf16 weight."""
-    rows, cols = int(pack["R"]), int(pack["C"])
-    bits = np.ascontiguousarray(pack["raw_bits"], dtype=np.uint16).reshape(rows, cols)
-    weight = torch.from_numpy(bits.view(np.int16).copy()).view(torch.bfloat16).to(torch.device(device))
-    return {"weight": weight, "R": rows, "C": cols, "codec": "raw", "format_version": FORMAT_VERSION, "layout": 0}
+    shape = (int(pack["R"]), int(pack["C"]))
+    return dict(weight=_bits_as_bf16(pack["raw_bits"], shape, device), R=shape[0], C=shape[1], codec="raw",
+                format_version=FORMAT_VERSION, layout=0)
 
 
 # ----------------------------------------------------------------- modules --

@@ -77,5 +77,6 @@ def test_the_json_line_carries_the_contract():
     cb = out["cpu_baseline"]
     for key in ("value", "unit", "cores", "kind", "sample", "legs"):
         assert key in cb, key
-    assert set(cb["legs"]) == {"all_cores", "one_thread", "cached_w"}
+    assert set(cb["legs"]) == {"cpu_share", "one_thread", "cached_w"}
+    assert cb["nproc"] >= 1 and 1 <= cb["cores"] <= min(cb["affinity_cpus"], 16)
     assert cb["legs"]["one_thread"]["cores"] == 1 and cb["kind"] in ("reference", "port")

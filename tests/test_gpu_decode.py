@@ -3,8 +3,9 @@
 
 Mirrors drinkme's device gate bench/radix_gemv_bitpin.py:86-116 (all 65,536
 bf16 patterns at every profile, 32- and 1024-weight blocks, bit-exact; the
-schedule equal to the CPU one) and tests/test_radix_bounds.py:149-182 (the
-device reader over a short block = the padded model)."""
+schedule equal to the CPU one). The device reader over a short block against
+the padded model (drinkme's tests/test_radix_bounds.py:149-182) is in
+tests/test_gpu_bounds.py."""
 
 import zlib
 

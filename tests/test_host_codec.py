@@ -98,17 +98,18 @@ def test_product_decoder_refuses_a_cut_terminal_and_bad_palette(rp):
         rp.decode(pal, off2, cut, 4, 1024, (3, 8))
     # decode trusts the palette, as drinkme's does (radix_native.cpp:173);
     # op 3 is the palette check, with the reference's wording
-    rp._native_call(3, None, 4, 1024, (3, 8), rp._tables_from_palette(pal, (3, 8)), None)
+    codec = rp.HostCodec(4, 1024, (3, 8))
+    codec.op(codec.CHECK_PALETTE, tables=rp.device_tables(pal, (3, 8)))
     for bad, why in ((np.zeros_like(pal), "invalid or repeated palette value"),):
         with pytest.raises(ValueError, match=why):
-            rp._native_call(3, None, 4, 1024, (3, 8), rp._tables_from_palette(bad, (3, 8)), None)
+            codec.op(codec.CHECK_PALETTE, tables=rp.device_tables(bad, (3, 8)))
         if O.ref_available():
             with pytest.raises(ValueError, match=why):
-                O._ref_call(3, None, 4, 1024, (3, 8), rp._tables_from_palette(bad, (3, 8)), None)
-    padded = rp._tables_from_palette(pal, (3, 8))
+                O._ref_call(3, None, 4, 1024, (3, 8), rp.device_tables(bad, (3, 8)), None)
+    padded = rp.device_tables(pal, (3, 8))
     padded[7] = 9
     with pytest.raises(ValueError, match="nonzero palette padding"):
-        rp._native_call(3, None, 4, 1024, (3, 8), padded, None)
+        codec.op(codec.CHECK_PALETTE, tables=padded)
 
 
 def _dict(rp, bits, profile="gulp"):
@@ -201,3 +202,27 @@ def test_qwen3_8b_step_has_253_gemvs_and_7_57g_weights():
     step = synth.qwen3_8b_step()
     assert len(step) == 253
     assert sum(r * c for _, _, r, c in step) == 36 * 192_937_984 + 151936 * 4096
+
+
+def test_device_tables_layout_closed_form(rp):
+    """Each nonterminal tier of width w takes ((1 << w) + 2) // 4 words
+    (src/drinkme/codec/radix_pack.py:333-350), its 2^w - 1 entries first
+    and zeros after, so the escape code 2^w - 1 reads a zero byte."""
+    rng = np.random.default_rng(5)
+    for widths in [(w, 8) for w in range(1, 9)] + [(2, 3, 8), (2, 2, 4, 8), (1, 4, 2, 8)]:
+        assert rp.table_words(widths) == sum(((1 << w) + 2) // 4 for w in widths[:-1])
+        cov = rp.covered_of(widths)
+        pal = rng.permutation(256)[:cov].astype(np.uint8) if cov <= 256 else None
+        if pal is None:
+            continue
+        t = rp.device_tables(pal, widths)
+        assert t.size == 4 * rp.table_words(widths)
+        at = base = 0
+        for w in widths[:-1]:
+            n = (1 << w) - 1
+            assert np.array_equal(t[at:at + n], pal[base:base + n])
+            assert not t[at + n:at + 4 * (((1 << w) + 2) // 4)].any()
+            assert t[at + n] == 0  # the escape code's byte
+            at += 4 * (((1 << w) + 2) // 4)
+            base += n
+        assert np.array_equal(rp.palette_of_tables(t, widths), pal)

@@ -79,3 +79,17 @@ def test_radix_module_refuses_a_cpu_device():
     d = oracle_dict(finite_bits(rng, (8, 1024)), "sip")
     with pytest.raises(ValueError, match="GPU"):
         swap.to_device_radix(d, "cpu")
+
+
+def test_to_device_raw_keeps_the_bits_in_a_copy_of_its_own():
+    import numpy as np
+
+    from drinkme_amd import radix_pack, swap
+
+    U = np.random.default_rng(3).integers(0, 1 << 16, (6, 1024), dtype=np.uint16)
+    rt = swap.to_device_raw(radix_pack.raw_dict(U), "cpu")
+    assert rt["codec"] == "raw" and (rt["R"], rt["C"]) == U.shape and rt["weight"].dtype == torch.bfloat16
+    got = rt["weight"].view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(got, U)
+    U[0, 0] ^= 1
+    assert got[0, 0] != U[0, 0], "the resident weight must not alias the pack's array"
