@@ -34,8 +34,19 @@ MC_MAX = 8  # src/drinkme/codec/ops.py:19
 _DTYPE = {torch.bfloat16: _native.DMX_BF16, torch.float32: _native.DMX_F32}
 
 
-def _stream():
-    return ct.c_void_p(torch.cuda.current_stream().cuda_stream)
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
+def _stream(device=None):
+    """The handle of torch's current stream on `device` (torch's current
+    device when None). torch's raw-handle accessor costs well under a
+    microsecond; torch.cuda.current_stream() builds a Stream object (about
+    3 us a call), which this falls back to only where the accessor is
+    missing."""
+    if _raw_stream is not None:
+        index = device.index if device is not None and device.index is not None else torch.cuda.current_device()
+        return _raw_stream(index)
+    return torch.cuda.current_stream(device).cuda_stream
 
 
 def descriptor(p: dict) -> _native.RadixTensor:
@@ -106,7 +117,7 @@ def _raw_rows(w: torch.Tensor, x: torch.Tensor, bias, out_dtype, what: str) -> t
     err = _native.error_buffer()
     st = _native.lib().dmx_gemv_narrow(w.data_ptr(), R, C, x.data_ptr(), xd, M,
                                        bias.data_ptr() if bias is not None else None, bd, out.data_ptr(), od,
-                                       _stream(), err, len(err))
+                                       _stream(x.device), err, len(err))
     _native.check(st, err, "dmx_gemv_narrow")
     return out
 
@@ -132,7 +143,7 @@ def _twin_rows(p: dict, x: torch.Tensor, bias, out_dtype) -> torch.Tensor:
     err = _native.error_buffer()
     st = _native.lib().dmx_radix_gemv_twin(w.data_ptr(), R, C, int(p.get("block_size", 1024)), len(widths), warr,
                                            x.data_ptr(), xd, M, bias.data_ptr() if bias is not None else None, bd,
-                                           out.data_ptr(), od, _stream(), err, len(err))
+                                           out.data_ptr(), od, _stream(x.device), err, len(err))
     _native.check(st, err, "dmx_radix_gemv_twin")
     return out
 
@@ -144,9 +155,11 @@ def gemv_rows(p: dict, x: torch.Tensor, bias=None, out_dtype=torch.float32) -> t
     if _is_twin(p):
         return _twin_rows(p, x, bias, out_dtype)
     R = int(p["R"])
-    M = _check_rows(x, int(p["C"]), p["rx_data"].device, bias, R, "radix gemv")
-    x = x.contiguous()
-    out = torch.empty((M, R), dtype=out_dtype, device=x.device)
+    dev = p["rx_data"].device
+    M = _check_rows(x, int(p["C"]), dev, bias, R, "radix gemv")
+    if not x.is_contiguous():
+        x = x.contiguous()
+    out = torch.empty((M, R), dtype=out_dtype, device=dev)
     xd = _dtype_code(x.dtype, "activation")
     od = _dtype_code(out_dtype, "output")
     if bias is not None:
@@ -157,7 +170,7 @@ def gemv_rows(p: dict, x: torch.Tensor, bias=None, out_dtype=torch.float32) -> t
     err = _native.error_buffer()
     st = _native.lib().dmx_radix_gemv(ct.byref(descriptor(p)), x.data_ptr(), xd, M,
                                        bias.data_ptr() if bias is not None else None, bd, out.data_ptr(), od,
-                                       _stream(), err, len(err))
+                                       _stream(dev), err, len(err))
     _native.check(st, err, "dmx_radix_gemv")
     return out
 
@@ -234,8 +247,8 @@ def gemv_group(ps, x: torch.Tensor, biases=None, out_dtype=torch.bfloat16) -> li
     tarr = (ct.POINTER(_native.RadixTensor) * n)(*[ct.pointer(d) for d in descs])
     oarr = (ct.c_void_p * n)(*[o.data_ptr() for o in outs])
     err = _native.error_buffer()
-    st = _native.lib().dmx_radix_gemv_group(tarr, n, x.data_ptr(), xd, M, bias_arr, bd, oarr, od, _stream(), err,
-                                             len(err))
+    st = _native.lib().dmx_radix_gemv_group(tarr, n, x.data_ptr(), xd, M, bias_arr, bd, oarr, od, _stream(x.device),
+                                             err, len(err))
     _native.check(st, err, "dmx_radix_gemv_group")
     return outs
 
@@ -248,7 +261,7 @@ def decode_bits(p: dict, num_warps: int | None = None) -> torch.Tensor:
     R, C = int(p["R"]), int(p["C"])
     out = torch.empty((R, C), dtype=torch.uint16, device=p["rx_data"].device)
     err = _native.error_buffer()
-    st = _native.lib().dmx_radix_decode(ct.byref(descriptor(p)), out.data_ptr(), _stream(), err, len(err))
+    st = _native.lib().dmx_radix_decode(ct.byref(descriptor(p)), out.data_ptr(), _stream(out.device), err, len(err))
     _native.check(st, err, "dmx_radix_decode")
     return out
 
@@ -277,7 +290,7 @@ def prepare_schedule(data, offsets, C: int, widths, B: int, nblocks: int) -> tor
         t.widths[i] = w
     sched = torch.zeros(int(nblocks), dtype=torch.uint16, device=data.device)
     err = _native.error_buffer()
-    st = _native.lib().dmx_radix_prepare(ct.byref(t), sched.data_ptr(), _stream(), err, len(err))
+    st = _native.lib().dmx_radix_prepare(ct.byref(t), sched.data_ptr(), _stream(sched.device), err, len(err))
     _native.check(st, err, "dmx_radix_prepare")
     return sched
 
