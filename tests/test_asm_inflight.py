@@ -212,8 +212,8 @@ def test_no_scratch_and_no_vgpr_spill_in_kernels_with_untracked_loads(kernel_asm
     wait would move registers the compiler thinks are ready; SGPR spills go
     to lanes of VGPRs (v_writelane / v_readlane), which the in-flight walk
     above watches like any other register write or read. So: no scratch
-    instruction, no VGPR spill and no AGPR in any of these kernels; SGPR
-    spills are counted and reported."""
+    instruction, no private segment, no VGPR spill and no AGPR in any of
+    these kernels; SGPR spills are counted and reported."""
     from tests.asm_inflight import metadata
 
     ks = kernels(kernel_asm, r"k_gemv_(sip|gulp)I")
@@ -223,6 +223,10 @@ def test_no_scratch_and_no_vgpr_spill_in_kernels_with_untracked_loads(kernel_asm
         assert name in md, f"{name}: no metadata"
         assert md[name].get("vgpr_spill_count", 0) == 0, f"{name}: {md[name]['vgpr_spill_count']} VGPR spills"
         assert "scratch_" not in body, f"{name}: scratch access"
+        # nor a private segment at all: a frame the compiler reserves (an SGPR spill slot it then
+        # placed in VGPR lanes) leaves no instruction but still has every dispatch set up scratch
+        assert md[name].get("private_segment_fixed_size", 0) == 0, \
+            f"{name}: {md[name]['private_segment_fixed_size']}-byte private segment"
         # the in-flight walk tracks VGPRs and SGPRs: a kernel that used AGPRs (as spill space, or an
         # MFMA's accumulators) would need the walk extended first
         assert md[name].get("agpr_count", 0) == 0 and not re.search(r"v_accvgpr|\ba\[?\d", body), \
