@@ -20,8 +20,11 @@ the activation rows (1 = decode, 4 = the MTP verify rows).
 A step is one sweep over the workload's GEMVs, captured once as a HIP graph
 and replayed; inputs are resident in HBM before timing starts. The GEMVs
 that share an activation in a decoder layer (q/k/v; gate/up) run as one
-grouped launch (dmx_radix_gemv_group), the others one launch each; the
-same sweep with one launch per GEMV is timed too (config.ungrouped).
+grouped launch (dmx_radix_gemv_group), the others one launch each. Also
+timed: the same sweep with one launch per GEMV (config.ungrouped), and
+without a graph, the way a serving loop calls it: one radix_ops call per
+Linear (config.eager_ungrouped), and one module call per Linear with the
+q/k/v and gate/up modules in shared-input groups (config.eager_modules).
 Reported:
   value       whole-sweep compressed-HBM GB/s = sum of algorithmic bytes /
               step time, B = 4 NW + 4 (R NB + 1) + P + 2 M C + 2 M R per
@@ -396,6 +399,26 @@ def main() -> int:
     ms_e, host_e = time_eager(sweep_eager, args.steps, args.warmup)
     log(f"sweep eager, one radix_ops call per Linear ({len(tensors)} launches): {ms_e * 1e3:.1f} us "
         f"({host_e * 1e3:.0f} us of host issue), {total_bytes / (ms_e * 1e-3) / 1e9:.0f} GB/s compressed")
+    # the module surface as a decoder layer calls it: one RadixCompressedLinear
+    # per Linear, called one by one on the layer's activation [1, M, C], with
+    # the q/k/v and gate/up modules joined by SharedInputGroup (one grouped
+    # launch each, the other members served from it), eagerly
+    from drinkme_amd import swap
+
+    mods = [swap.RadixCompressedLinear(t["rt"]) for t in tensors]
+    for grp in groups:
+        if len(grp) > 1:
+            swap.SharedInputGroup([mods[i] for i in grp])
+    xin = {c: x.reshape(1, args.m, c) for c, x in xs.items()}
+
+    def sweep_modules():
+        for mod, t in zip(mods, tensors):
+            mod(xin[t["C"]])
+
+    ms_md, host_md = time_eager(sweep_modules, args.steps, args.warmup)
+    log(f"sweep eager, one module call per Linear, q/k/v and gate/up grouped ({len(groups)} launches): "
+        f"{ms_md * 1e3:.1f} us ({host_md * 1e3:.0f} us of host issue), "
+        f"{total_bytes / (ms_md * 1e-3) / 1e9:.0f} GB/s compressed")
     traffic = None
     tf = os.path.join(ROOT, "profiles", "traffic.json")
     key = f"k_gemv_{args.profile} {dom_shape} {args.profile} M={args.m}"
@@ -436,6 +459,11 @@ def main() -> int:
                                 "value": round(total_bytes / (ms_e * 1e-3) / 1e9, 1),
                                 "host_issue_us_per_sweep": round(host_e * 1e3, 1),
                                 "calls": "radix_ops.gemv_fused per Linear (gemv_rows at M > 1), eager, no graph"},
+            "eager_modules": {"launches": len(groups), "us_per_sweep": round(ms_md * 1e3, 2),
+                              "value": round(total_bytes / (ms_md * 1e-3) / 1e9, 1),
+                              "host_issue_us_per_sweep": round(host_md * 1e3, 1),
+                              "calls": "one RadixCompressedLinear call per Linear on x [1, M, C], q/k/v and gate/up "
+                                       "joined by swap.SharedInputGroup, eager, no graph"},
             "timing": "HIP graph of the sweep, replayed; events around the timed replays",
             "weights_rng": f"dmx_synth_bf16 seed {synth.SEED}, one stream per (workload, layer, tensor)",
         },

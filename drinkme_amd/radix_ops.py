@@ -24,6 +24,7 @@ allocates only its output, with torch.
 from __future__ import annotations
 
 import ctypes as ct
+import threading
 
 import torch
 
@@ -75,6 +76,26 @@ def descriptor(p: dict) -> _native.RadixTensor:
             t.widths[i] = w
         p["_dmx"] = (key, t)
     return t
+
+
+_tls = threading.local()
+
+
+def _error_buffer():
+    """This thread's error buffer for the launchers below (the library
+    writes into it only when a call fails)."""
+    buf = getattr(_tls, "err", None)
+    if buf is None:
+        buf = _tls.err = _native.error_buffer()
+    return buf
+
+
+def _buffers(p: dict) -> tuple:
+    return p["rx_data"], p["rx_offsets"], p["rx_palette"], p.get("rx_schedule")
+
+
+def _same_buffers(a: tuple, b: tuple) -> bool:
+    return a[0] is b[0] and a[1] is b[1] and a[2] is b[2] and a[3] is b[3]
 
 
 def _dtype_code(dtype, what):
@@ -175,6 +196,63 @@ def gemv_rows(p: dict, x: torch.Tensor, bias=None, out_dtype=torch.float32) -> t
     return out
 
 
+def _leading_rows(x: torch.Tensor, C: int, device, what: str) -> int:
+    """M, the rows of x [..., C] (the product of its leading dimensions),
+    after the checks every launcher makes."""
+    if x.dim() == 0 or x.shape[-1] != C:
+        raise ValueError(f"{what}: x must be [..., {C}], got {tuple(x.shape)}")
+    M = x.numel() // C
+    if not 1 <= M <= MC_MAX:
+        raise ValueError(f"{what}: M={M} outside 1..{MC_MAX}")
+    if x.device != device:
+        raise ValueError(f"{what}: x is not on the weight's device")
+    return M
+
+
+class RowsLauncher:
+    """dmx_radix_gemv for one radix tensor that a caller (a module) launches
+    again and again: its descriptor is built once, and again only when the
+    runtime dict holds other buffers than at the last call. call(x, bias,
+    out_dtype): x [..., C] (bf16 or fp32; M, the product of the leading
+    dimensions, in 1..MC_MAX) -> [..., R] in out_dtype, gemv_rows' result
+    bit for bit."""
+
+    def __init__(self, p: dict):
+        if _is_twin(p):
+            raise ValueError("RowsLauncher: a radix runtime dict, not a twin")
+        self.p = p
+        self.R, self.C = int(p["R"]), int(p["C"])
+        self.device = p["rx_data"].device
+        self._held = None
+
+    def _pointer(self):
+        held = _buffers(self.p)
+        if self._held is None or not _same_buffers(held, self._held):
+            self._ptr = ct.pointer(descriptor(self.p))
+            self._held = held
+        return self._ptr
+
+    def __call__(self, x: torch.Tensor, bias=None, out_dtype=torch.float32) -> torch.Tensor:
+        M = _leading_rows(x, self.C, self.device, "radix gemv")
+        if not x.is_contiguous():
+            x = x.contiguous()
+        xd = _dtype_code(x.dtype, "activation")
+        od = _dtype_code(out_dtype, "output")
+        bd = 0
+        if bias is not None:
+            if bias.numel() != self.R or bias.device != x.device:
+                raise ValueError("radix gemv: bias must hold R elements on the weight's device")
+            bias = bias.contiguous()
+            bd = _dtype_code(bias.dtype, "bias")
+        out = torch.empty((*x.shape[:-1], self.R), dtype=out_dtype, device=self.device)
+        err = _error_buffer()
+        st = _native.lib().dmx_radix_gemv(self._pointer(), x.data_ptr(), xd, M,
+                                           bias.data_ptr() if bias is not None else None, bd, out.data_ptr(), od,
+                                           _stream(self.device), err, len(err))
+        _native.check(st, err, "dmx_radix_gemv")
+        return out
+
+
 def gemv_narrow(w: torch.Tensor, x: torch.Tensor, bias, block: int = 512, num_warps: int = 4) -> torch.Tensor:
     """swap.NarrowLinear's forward for 1 <= M <= 8 rows (radix_ops.py:
     401-415): x [M, C] (bf16 or fp32) against the row-major bf16 weight
@@ -202,55 +280,114 @@ def gemv_mc(p: dict, x: torch.Tensor) -> torch.Tensor:
     return gemv_rows(p, x, None, torch.float32)
 
 
+class GroupLauncher:
+    """dmx_radix_gemv_group over a fixed list of radix tensors that share
+    the activation (a layer's q/k/v or gate/up), with the descriptor array
+    built once: call(x, biases, out_dtype) for x [..., C] -> one [..., R_i]
+    output per tensor, each as gemv_rows would give it (within the same
+    float64 bound), in one launch. The descriptors are rebuilt when a
+    tensor's runtime dict holds other buffers than at the last call, the
+    bias array when the biases are other tensors."""
+
+    def __init__(self, ps):
+        ps = list(ps)
+        if not ps:
+            raise ValueError("radix gemv_group: no tensors")
+        if any(_is_twin(p) for p in ps):
+            raise ValueError("radix gemv_group: twin dicts launch one GEMV each")
+        self.ps = ps
+        self.C = int(ps[0]["C"])
+        if any(int(p["C"]) != self.C for p in ps):
+            raise ValueError(f"radix gemv_group: every tensor needs C = {self.C}")
+        self.device = ps[0]["rx_data"].device
+        if any(p["rx_data"].device != self.device for p in ps):
+            raise ValueError("radix gemv_group: the tensors are on different devices")
+        self.R = [int(p["R"]) for p in ps]
+        self._held = None
+        self._bias_key = None
+
+    def _table(self):
+        """The descriptor pointer array, rebuilt when a dict's buffers are no
+        longer the ones it was built from."""
+        held = [_buffers(p) for p in self.ps]
+        if self._held is None or not all(_same_buffers(a, b) for a, b in zip(held, self._held)):
+            descs = [descriptor(p) for p in self.ps]
+            self._tarr = (ct.POINTER(_native.RadixTensor) * len(descs))(*[ct.pointer(d) for d in descs])
+            self._descs = descs  # the array points into these
+            self._held = held
+        return self._tarr
+
+    def _bias_array(self, biases, x):
+        """(pointer array, dtype code, the biases it points into); kept while
+        the same contiguous bias tensors come back."""
+        key = tuple(biases)
+        if self._bias_key is not None and len(key) == len(self._bias_key) and \
+                all(a is b for a, b in zip(key, self._bias_key)):
+            return self._bias_cached
+        n = len(self.ps)
+        if len(biases) != n:
+            raise ValueError("radix gemv_group: one bias (or None) per tensor")
+        biases = [None if b is None else b.contiguous() for b in biases]
+        dts = {b.dtype for b in biases if b is not None}
+        if len(dts) > 1:
+            raise ValueError("radix gemv_group: the biases must share a dtype")
+        for b, R in zip(biases, self.R):
+            if b is not None and (b.numel() != R or b.device != x.device):
+                raise ValueError("radix gemv_group: bias must hold R elements on the weight's device")
+        bd = _dtype_code(dts.pop(), "bias") if dts else 0
+        cached = (ct.c_void_p * n)(*[None if b is None else b.data_ptr() for b in biases]), bd, biases
+        if all(b is None or b is c for b, c in zip(key, biases)):  # (no copies made: the same tensors next time)
+            self._bias_key, self._bias_cached = key, cached
+        return cached
+
+    def __call__(self, x: torch.Tensor, biases=None, out_dtype=torch.bfloat16) -> list:
+        if x.dim() == 0 or x.shape[-1] != self.C:
+            raise ValueError(f"radix gemv_group: every tensor needs C = {self.C} and x [..., {self.C}]")
+        M = x.numel() // self.C
+        if not 1 <= M <= MC_MAX:
+            raise ValueError(f"radix gemv_group: M={M} outside 1..{MC_MAX}")
+        if x.device != self.device:
+            raise ValueError("radix gemv_group: x is not on the weights' device")
+        if not x.is_contiguous():
+            x = x.contiguous()
+        xd = _dtype_code(x.dtype, "activation")
+        od = _dtype_code(out_dtype, "output")
+        bias_arr, bd = None, 0
+        if biases is not None and any(b is not None for b in biases):
+            bias_arr, bd, biases = self._bias_array(biases, x)  # (the contiguous biases live through the call)
+        tarr = self._table()
+        lead = x.shape[:-1]
+        outs = [torch.empty((*lead, R), dtype=out_dtype, device=self.device) for R in self.R]
+        n = len(outs)
+        oarr = (ct.c_void_p * n)(*[o.data_ptr() for o in outs])
+        err = _error_buffer()
+        st = _native.lib().dmx_radix_gemv_group(tarr, n, x.data_ptr(), xd, M, bias_arr, bd, oarr, od,
+                                                 _stream(self.device), err, len(err))
+        _native.check(st, err, "dmx_radix_gemv_group")
+        return outs
+
+
 def gemv_group(ps, x: torch.Tensor, biases=None, out_dtype=torch.bfloat16) -> list:
     """Several radix tensors that share the activation (a layer's q/k/v or
     gate/up): x [M, C] or [C] -> one [M, R_i] output per tensor, each as
     gemv_rows would give it (within the same float64 bound), as one launch
-    where the kernels allow (dmx_radix_gemv_group). No drinkme counterpart:
-    drinkme launches one GEMV per Linear."""
+    where the kernels allow (dmx_radix_gemv_group; twin dicts launch one
+    GEMV each). No drinkme counterpart: drinkme launches one GEMV per
+    Linear."""
     ps = list(ps)
-    if not ps:
-        raise ValueError("radix gemv_group: no tensors")
-    if x.dim() == 1:
-        x = x.reshape(1, -1)
-    C = int(ps[0]["C"])
-    if x.dim() != 2 or x.shape[1] != C or any(int(p["C"]) != C for p in ps):
-        raise ValueError(f"radix gemv_group: every tensor needs C = {C} and x [M, {C}]")
-    M = x.shape[0]
-    if not 1 <= M <= MC_MAX:
-        raise ValueError(f"radix gemv_group: M={M} outside 1..{MC_MAX}")
-    if any(_is_twin(p) for p in ps):  # raw weights: one launch each
+    if ps and any(_is_twin(p) for p in ps):  # raw weights: one launch each
+        if x.dim() == 1:
+            x = x.reshape(1, -1)
+        C = int(ps[0]["C"])
+        if x.dim() != 2 or x.shape[1] != C or any(int(p["C"]) != C for p in ps):
+            raise ValueError(f"radix gemv_group: every tensor needs C = {C} and x [M, {C}]")
+        if not 1 <= x.shape[0] <= MC_MAX:
+            raise ValueError(f"radix gemv_group: M={x.shape[0]} outside 1..{MC_MAX}")
         bl = list(biases) if biases is not None else [None] * len(ps)
         return [gemv_rows(p, x, b, out_dtype) for p, b in zip(ps, bl)]
-    if any(x.device != p["rx_data"].device for p in ps):
+    if ps and any(p["rx_data"].device != x.device for p in ps):
         raise ValueError("radix gemv_group: x is not on the weights' device")
-    x = x.contiguous()
-    xd = _dtype_code(x.dtype, "activation")
-    od = _dtype_code(out_dtype, "output")
-    outs = [torch.empty((M, int(p["R"])), dtype=out_dtype, device=x.device) for p in ps]
-    n = len(ps)
-    bias_arr, bd = None, 0
-    if biases is not None:
-        biases = [None if b is None else b.contiguous() for b in biases]
-        if len(biases) != n:
-            raise ValueError("radix gemv_group: one bias (or None) per tensor")
-        dts = {b.dtype for b in biases if b is not None}
-        if len(dts) > 1:
-            raise ValueError("radix gemv_group: the biases must share a dtype")
-        for b, p in zip(biases, ps):
-            if b is not None and (b.numel() != int(p["R"]) or b.device != x.device):
-                raise ValueError("radix gemv_group: bias must hold R elements on the weight's device")
-        if dts:
-            bd = _dtype_code(dts.pop(), "bias")
-        bias_arr = (ct.c_void_p * n)(*[None if b is None else b.data_ptr() for b in biases])
-    descs = [descriptor(p) for p in ps]
-    tarr = (ct.POINTER(_native.RadixTensor) * n)(*[ct.pointer(d) for d in descs])
-    oarr = (ct.c_void_p * n)(*[o.data_ptr() for o in outs])
-    err = _native.error_buffer()
-    st = _native.lib().dmx_radix_gemv_group(tarr, n, x.data_ptr(), xd, M, bias_arr, bd, oarr, od, _stream(x.device),
-                                             err, len(err))
-    _native.check(st, err, "dmx_radix_gemv_group")
-    return outs
+    return GroupLauncher(ps)(x.reshape(1, -1) if x.dim() == 1 else x, biases, out_dtype)
 
 
 def decode_bits(p: dict, num_warps: int | None = None) -> torch.Tensor:

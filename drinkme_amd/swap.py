@@ -17,6 +17,10 @@ Contract kept from drinkme (src/drinkme/codec/swap.py):
     and make_module (:900-919).
 There is no CPU route: every arm runs on the GPU, and an activation on the
 CPU is refused.
+
+Added here, with no drinkme counterpart: SharedInputGroup / install_groups,
+which let a layer's q/k/v (and gate/up) modules, still called one by one,
+share one grouped launch.
 """
 
 from __future__ import annotations
@@ -187,6 +191,8 @@ def to_device_raw(pack: dict, device: str = "cuda") -> dict:
 
 # ----------------------------------------------------------------- modules --
 
+_KERNEL_DTYPES = (torch.bfloat16, torch.float32)  # activations the kernels take as they are
+
 
 class RadixCompressedLinear(torch.nn.Module):
     """A radix-coded Linear resident on the GPU (`p` is its runtime dict).
@@ -213,6 +219,8 @@ class RadixCompressedLinear(torch.nn.Module):
         self.layout = 0
         self._arms = {"gemv": self._rows_arm, "mc": self._rows_arm, "dense": self._dense_arm,
                       "loop": self._loop_arm}
+        self._launch = radix_ops.RowsLauncher(runtime)  # the gemv and mc arms' launch, its descriptor kept
+        self._group, self._slot = None, -1  # a SharedInputGroup this module serves in, and its place there
 
     def _route(self, x) -> str:
         """The arm for x: "cpu" off the GPU, else by its row count (the
@@ -229,6 +237,10 @@ class RadixCompressedLinear(torch.nn.Module):
     def _forward(self, x, route: str):
         if route == "cpu":
             raise RuntimeError("RadixCompressedLinear: the radix arms run on the GPU; x is on the CPU")
+        if route in ("gemv", "mc") and x.dtype in _KERNEL_DTYPES:  # (output in x's shape, no reshapes)
+            if self._group is not None:
+                return self._group.rows(self._slot, x)
+            return self._launch(x, self.bias, x.dtype)
         rows = x.reshape(-1, self.C)
         y = self._arms[route](rows, x.dtype)
         return y.reshape(*x.shape[:-1], self.R)
@@ -238,7 +250,7 @@ class RadixCompressedLinear(torch.nn.Module):
         return (y32 if self.bias is None else y32 + self.bias).to(dtype)
 
     def _rows_arm(self, rows, dtype):
-        if dtype in (torch.bfloat16, torch.float32):
+        if dtype in _KERNEL_DTYPES:
             return radix_ops.gemv_rows(self.p, rows, self.bias, dtype)
         return self._round_once(radix_ops.gemv_rows(self.p, rows.float(), None, torch.float32), dtype)
 
@@ -281,6 +293,105 @@ def make_module(pack: dict, bias=None, device="cuda") -> torch.nn.Module:
         raise ValueError(f"make_module: codec {codec!r} is not a radix or raw tensor")
     module, resident = kinds[codec]
     return module(resident(pack, device), bias)
+
+
+# ------------------------------------------------- shared-input groups --
+
+
+class SharedInputGroup:
+    """RadixCompressedLinear modules that read one activation (a decoder
+    layer's q/k/v projections, or its gate/up), served by one grouped launch
+    (dmx_radix_gemv_group) where drinkme launches one GEMV per module
+    (swap.py:443-456). The callers keep calling each module as before.
+
+    The first member called with an activation launches the GEMVs of every
+    member and keeps the other members' rows; a member called next with
+    that same activation takes its rows from the launch. "That same
+    activation" means the same tensor object, with torch's version counter
+    unchanged since the launch (no in-place write through torch), the same
+    row count, on the same stream and under the same graph-capture state.
+    The group holds the activation until every member has taken its rows,
+    so its memory cannot pass to another tensor meanwhile. Anything else (a
+    member called twice, another activation, an in-place write) launches
+    again, so each call returns what the module's own launch would (the
+    grouped kernels' sums, within the same float64 bound as one GEMV each).
+    Not seen: a write into the activation that bypasses torch (a kernel
+    given its raw address), or any in-place write to an inference-mode
+    tensor (torch keeps no version counter for those); a caller that does
+    either between the members' calls calls reset() first."""
+
+    def __init__(self, members):
+        members = list(members)
+        if len(members) < 2:
+            raise ValueError("SharedInputGroup: at least two modules")
+        for m in members:
+            if not isinstance(m, RadixCompressedLinear):
+                raise TypeError(f"SharedInputGroup: {type(m).__name__} is not a RadixCompressedLinear")
+            if m._group is not None:
+                raise ValueError("SharedInputGroup: a module is already in a group")
+        if len({id(m) for m in members}) != len(members):
+            raise ValueError("SharedInputGroup: a module appears twice")
+        self.launch = radix_ops.GroupLauncher([m.p for m in members])
+        self.members = members
+        for slot, m in enumerate(members):
+            m._group, m._slot = self, slot
+        self.reset()
+
+    def reset(self) -> None:
+        """Drops the rows held for members not yet called."""
+        self._x, self._key, self._outs = None, None, None
+
+    def dissolve(self) -> None:
+        """Returns every member to one launch per call."""
+        for m in self.members:
+            m._group, m._slot = None, -1
+        self.reset()
+
+    @staticmethod
+    def _match(x, m: int):
+        version = None if x.is_inference() else x._version
+        return (m, version, radix_ops._stream(x.device), torch.cuda.is_current_stream_capturing())
+
+    def rows(self, slot: int, x: torch.Tensor) -> torch.Tensor:
+        """Member `slot`'s rows of activation x [..., C]: [..., R] in x's
+        dtype."""
+        key = self._match(x, x.numel())
+        outs = self._outs
+        if outs is None or x is not self._x or key != self._key or outs[slot] is None:
+            outs = self.launch(x, [m.bias for m in self.members], x.dtype)
+            self._x, self._key, self._outs = x, key, outs
+        y, outs[slot] = outs[slot], None
+        if all(o is None for o in outs):
+            self.reset()
+        return y
+
+
+SIBLINGS = (("q_proj", "k_proj", "v_proj"), ("gate_proj", "up_proj"))  # children that read one activation
+
+
+def install_groups(model, sets=SIBLINGS) -> list:
+    """Groups, in place, the RadixCompressedLinear children of each module
+    of `model` named in one entry of `sets` (at least two present, with one
+    column count, device and bias dtype, none grouped yet) into a
+    SharedInputGroup; returns the qualified names of each group. Run it
+    after the Linears are swapped; nothing else about the modules changes.
+    No drinkme counterpart: drinkme launches one GEMV per module."""
+    made = []
+    for prefix, parent in model.named_modules():
+        kids = dict(parent.named_children())
+        for names in sets:
+            picked = [(n, kids[n]) for n in names
+                      if isinstance(kids.get(n), RadixCompressedLinear) and kids[n]._group is None]
+            if len(picked) < 2:
+                continue
+            mods = [m for _, m in picked]
+            bias_dtypes = {m.bias.dtype for m in mods if m.bias is not None}
+            if (len({m.C for m in mods}) != 1 or len({m.p["rx_data"].device for m in mods}) != 1
+                    or len(bias_dtypes) > 1):
+                continue
+            SharedInputGroup(mods)
+            made.append(tuple(f"{prefix}.{n}" if prefix else n for n, _ in picked))
+    return made
 
 
 # ------------------------------------------------------- the raw Linears --

@@ -69,6 +69,8 @@ def test_the_json_line_carries_the_contract():
     # value is the sweep's algorithmic bytes over its time
     c = out["config"]
     assert abs(out["value"] - c["compressed_bytes"] / (out["ms_per_step"] * 1e-3) / 1e9) <= 0.01 * out["value"]
+    for k in ("ungrouped", "eager_ungrouped", "eager_modules"):
+        assert c[k]["us_per_sweep"] > 0 and c[k]["launches"] >= 1, k
     r = out["roofline"]
     assert r["bound"] == "hbm" and r["unit"] == "GB/s" and r["peak"] == 8000.0
     assert abs(r["frac"] - r["achieved"] / r["peak"]) < 1e-3
