@@ -525,6 +525,7 @@ struct SipGroup {
     void* out[kGroupMax];
     uint32_t row0[kGroupMax + 1];  // row0[n] = the group's row count
 };
+static_assert(sizeof(SipGroup) + 8 + sizeof(SipShape) <= 5 * 64, "the sip and gulp arguments span five lines");
 
 // arr[i] for a wave-uniform i < kGroupMax, by selects (no indexed copy of
 // the kernel arguments).
@@ -551,6 +552,19 @@ struct SipStage {
 // The directory, read-only for the whole launch: through the constant
 // address space its wave-uniform reads become scalar loads.
 typedef const __attribute__((address_space(4))) uint32_t* const_u32_ptr;
+
+// The kernel arguments of the sip and gulp kernels (SipGroup, x, SipShape:
+// 296 bytes) lie in five 64-byte lines of the argument segment. The
+// prologue reads them in several batches, each waited on before the next
+// (the placement needs the shape, the tensor pointers need the placement),
+// and each batch's first read of a line costs a round trip to memory.
+// Reading one word of every line here, in one batch with one wait, brings
+// them all into the scalar cache at once; the later reads hit there.
+__device__ __forceinline__ void touch_kernel_args() {
+    const const_u32_ptr ka = (const_u32_ptr)__builtin_amdgcn_kernarg_segment_ptr();
+    const uint32_t a0 = ka[0], a1 = ka[16], a2 = ka[32], a3 = ka[48], a4 = ka[64];
+    asm volatile("" ::"s"(a0), "s"(a1), "s"(a2), "s"(a3), "s"(a4));
+}
 
 // A block's directory pair, read through the scalar cache. (The byte
 // offset is 32-bit, so the load takes it in an SGPR with no 64-bit address
@@ -742,6 +756,7 @@ void k_gemv_sip(const SipGroup g, const uint16_t* __restrict__ x, const SipShape
     __shared__ uint32_t wg_done;  // blocks the workgroup's waves have started (progress balance)
     __shared__ uint2 sel2[13 * 16];
     extern __shared__ __align__(16) uint8_t lds_dyn[];
+    touch_kernel_args();
     uint16_t* xs = reinterpret_cast<uint16_t*>(lds_dyn);
     // (a multiple of 8 bf16, stated so that 16-byte LDS reads of the rows stay whole)
     const uint32_t xrow = sh.xrow & ~7u;
@@ -1392,6 +1407,7 @@ void k_gemv_gulp(const SipGroup g, const uint16_t* __restrict__ x, const SipShap
     __shared__ uint32_t pal2w[4];
     __shared__ uint32_t x2_all[kSipWaves * kGulpX2Words];
     extern __shared__ __align__(16) uint8_t lds_dyn[];
+    touch_kernel_args();
     uint16_t* xs = reinterpret_cast<uint16_t*>(lds_dyn);
     // (a multiple of 8 bf16, stated so that 16-byte LDS reads of the rows stay whole)
     const uint32_t xrow = sh.xrow & ~7u;
