@@ -589,38 +589,38 @@ __device__ __forceinline__ i32x4 make_rsrc(const void* base, uint32_t bytes) {
     return r;
 }
 
-// A block's loads through its tensor's buffer resource (based at the
-// workgroup's first block of that tensor, so every byte offset is small),
-// non-temporal (`nt`): a sweep reads each weight once, and keeping the
-// stream out of the caches measured 2.7% faster on the Qwen3-8B step:
-// the terminal word, the tier-0 pair and the literals, issued as one unit of
-// three vector loads. They are written as instructions the compiler does
-// not track, so the only waits on them are the explicit SIP_WAIT below,
-// placed where a stage is consumed: loads return in issue order, so waiting
-// until at most N newer loads are outstanding completes the stage, whatever
-// other loads the compiler adds after it. Every read lies within the
-// block's start + 352 + 64 words, inside block_word_bounds(1024)[1] = 608.
-// The terminal word goes through a resource spanning the block alone: a
-// lane past the block's last word reads 0 and fetches nothing (loading it
-// from the next block's literals, fetched again with that block, made the
-// traffic 7% above the block bytes; bitwise the same outputs, the Qwen3-8B
-// step 3.2% faster).
-__device__ __forceinline__ SipStage sip_load(i32x4 rsrc, uint32_t base, uint2 o, uint32_t t, const SipLanes& ln,
-                                             const uint32_t* data) {
+// A block's loads, non-temporal (`nt`): a sweep reads each weight once, and
+// keeping the stream out of the caches measured 2.7% faster on the Qwen3-8B
+// step: the terminal word, the tier-0 pair and the literals, issued as one
+// unit of three vector loads. They are written as instructions the compiler
+// does not track, so the only waits on them are the explicit SIP_WAIT
+// below, placed where a stage is consumed: loads return in issue order, so
+// waiting until at most N newer loads are outstanding completes the stage,
+// whatever other loads the compiler adds after it.
+// The terminal goes through a buffer resource spanning the block alone
+// ([start, end) of its directory pair): a lane past the block's last word
+// reads 0 and fetches nothing. That keeps the next block's literals from
+// being fetched twice (the traffic was 7% above the block bytes that way;
+// bitwise the same outputs, the Qwen3-8B step 3.2% faster). The literal
+// and tier-0 reads (the block's first 352 words) go through one from the
+// block's start with no end, as drinkme's readers take a block cut shorter
+// than that: the words after it. A stage past the wave's work comes with a
+// zero-length pair (end = start) and both resources empty: nothing of it
+// is fetched, and the stage is only waited on.
+__device__ __forceinline__ SipStage sip_load(uint2 o, uint32_t t, const SipLanes& ln, const uint32_t* data) {
     SipStage s;
     s.start = o.x;
     s.end = o.y;
     s.t = t;
-    const uint32_t soff = (o.x - base) * 4u;
-    // the terminal through a resource of the block's own extent: a lane past
-    // the block's last word reads 0 and fetches nothing
     const i32x4 rterm = make_rsrc(data + o.x, (o.y - o.x) * 4u);
+    i32x4 rfix = rterm;
+    rfix.z = o.y != o.x ? 0x7FFFFFFF : 0;
     asm volatile(
-        "buffer_load_dword %0, %3, %8, 0 offen nt\n\t"
-        "buffer_load_dwordx2 %1, %4, %6, %7 offen nt\n\t"
-        "buffer_load_dwordx4 %2, %5, %6, %7 offen nt"
+        "buffer_load_dword %0, %3, %6, 0 offen nt\n\t"
+        "buffer_load_dwordx2 %1, %4, %7, 0 offen nt\n\t"
+        "buffer_load_dwordx4 %2, %5, %7, 0 offen nt"
         : "=&v"(s.term), "=&v"(s.t0), "=&v"(s.lit)
-        : "v"(ln.term), "v"(ln.t0), "v"(ln.lit), "s"(rsrc), "s"(soff), "s"(rterm));
+        : "v"(ln.term), "v"(ln.t0), "v"(ln.lit), "s"(rterm), "s"(rfix));
     return s;
 }
 
@@ -783,7 +783,8 @@ void k_gemv_sip(const SipGroup g, const uint16_t* __restrict__ x, const SipShape
     if constexpr (!DEC) load_x_slice<M>(sh, x, xs, 0, kSipThreads);
 
     // the first two blocks' loads go out before the tables are built; a
-    // cursor past the wave's work reads the workgroup's first block instead
+    // cursor past the wave's work reads the workgroup's first directory
+    // entry and, through a zero-length window, no payload
     SipCursor p;
     QuadCursor pq;
     const SipWalk wk = sip_walk<QUAD>(sh, nrows);
@@ -813,18 +814,20 @@ void k_gemv_sip(const SipGroup g, const uint16_t* __restrict__ x, const SipShape
             nr.last = p.j + 1 == sh.seg_blocks;
         }
         uint2 o;
-        if constexpr (RAW)  // the block's byte offset from the workgroup's first row
+        if constexpr (RAW) {  // the block's byte offset from the workgroup's first row
             o = make_uint2((is.blk - sp.a_first) * 2048u, 0u);
-        else
+        } else {
             o = sip_offsets(TWO && is.t ? offsets_b : offsets_a, is.blk);
+            if (!is.live) o.y = o.x;  // (past the work: a zero-length window, nothing fetched)
+        }
         if constexpr (QUAD)
             quad_next(sh, pq, wk);
         else
             sip_next<TWO>(sh, p, wk, sp);
         return o;
     };
-    // the first blocks' directory entries, then the payload windows' bases:
-    // all issued before any is waited on (one round trip, not two)
+    // the first blocks' directory entries, all issued before any is waited
+    // on (one round trip)
     const uint2 oA = next_offsets();
     SipRef rA = nr;
     const uint2 oB = next_offsets();
@@ -837,19 +840,13 @@ void k_gemv_sip(const SipGroup g, const uint16_t* __restrict__ x, const SipShape
         oD = next_offsets();
         rD = nr;
     }
-    // each tensor's payload window: from the workgroup's first block of it
-    // (the raw twin: from the workgroup's first row, 512 words a block)
-    uint32_t base_a = 0, base_b = 0;
-    if constexpr (!RAW) {
-        base_a = ((const_u32_ptr)offsets_a)[sp.a_first];
-        base_b = ((const_u32_ptr)offsets_b)[0];
-    }
-    const i32x4 rsrc_a = make_rsrc(RAW ? data_a + (uint64_t)sp.a_first * 512u : data_a + base_a, 0x7FFFFFFFu);
-    const i32x4 rsrc_b = make_rsrc(data_b + base_b, 0x7FFFFFFFu);
+    // the raw twin's window: from the workgroup's first row, 512 words a
+    // block (the compressed blocks load through windows of their own)
+    const i32x4 rsrc_a = make_rsrc(data_a + (uint64_t)sp.a_first * 512u, 0x7FFFFFFFu);
     const SipLanes ln = sip_lanes(lane);
     auto load = [&](uint2 o, uint32_t t) {
         if constexpr (RAW) return raw_load(rsrc_a, o.x, ln);
-        return TWO && t ? sip_load(rsrc_b, base_b, o, 1u, ln, data_b) : sip_load(rsrc_a, base_a, o, 0u, ln, data_a);
+        return TWO && t ? sip_load(o, 1u, ln, data_b) : sip_load(o, 0u, ln, data_a);
     };
     // the prologue's stages issue in the loop's order (no interleaving),
     // so the waits the loop needs are the same on entry as in steady state
