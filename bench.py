@@ -370,13 +370,19 @@ def main() -> int:
     log(f"dominant launch {dom_shape}: {dom_us:.2f} us/launch, {achieved:.0f} GB/s ({achieved / PEAK_GBPS:.1%} of peak), "
         f"{round(dom_bytes)} algorithmic bytes per launch")
     if args.kernel_only:
-        # a plain copy of known size beside it: the scale for counter-derived bytes
+        # a plain copy of known size beside it: the scale for counter-derived
+        # bytes; then reductions over the same 256 MiB, a second scale for
+        # the read counter from a kernel that only reads
         src = torch.empty(64 * 2**20, dtype=torch.float32, device="cuda").fill_(1.0)
         dst = torch.empty_like(src)
         for _ in range(3):
             dst.copy_(src)
         torch.cuda.synchronize()
         log("calibration copy: 3 x 256 MiB device-to-device")
+        for _ in range(3):
+            src.sum()
+        torch.cuda.synchronize()
+        log("calibration read: 3 sums over 256 MiB")
         return 0
     ms = time_graph(sweep, args.steps, args.warmup)
     value = total_bytes / (ms * 1e-3) / 1e9
