@@ -25,6 +25,8 @@ timed: the same sweep with one launch per GEMV (config.ungrouped), and
 without a graph, the way a serving loop calls it: one radix_ops call per
 Linear (config.eager_ungrouped), and one module call per Linear with the
 q/k/v and gate/up modules in shared-input groups (config.eager_modules).
+For gulp at M = 3..4 the sweep is also timed with its verify rows on the
+matrix cores (radix_ops.set_policy("matrix"), config.matrix_cores).
 Reported:
   value       whole-sweep compressed-HBM GB/s = sum of algorithmic bytes /
               step time, B = 4 NW + 4 (R NB + 1) + P + 2 M C + 2 M R per
@@ -388,6 +390,20 @@ def main() -> int:
     value = total_bytes / (ms * 1e-3) / 1e9
     log(f"sweep ({len(groups)} launches): {ms * 1e3:.1f} us, {value:.0f} GB/s compressed ({value / PEAK_GBPS:.1%}), "
         f"{total_bf16 / (ms * 1e-3) / 1e9:.0f} GB/s bf16-equivalent")
+    # gulp's 3- and 4-row verify: AUTO runs it on v_dot2 (measured faster);
+    # the matrix policy runs it in quad units on the matrix cores, as 8 rows
+    # run: the same sweep timed on that path too
+    matrix = None
+    if args.profile == "gulp" and args.m in (3, 4):
+        prev = radix_ops.set_policy("matrix")
+        try:
+            ms_mx = time_graph(sweep, args.steps, args.warmup)
+        finally:
+            radix_ops.set_policy(prev)
+        matrix = {"us_per_sweep": round(ms_mx * 1e3, 2), "value": round(total_bytes / (ms_mx * 1e-3) / 1e9, 1),
+                  "path": "radix_ops.set_policy('matrix'): the verify rows in quad units on the matrix cores "
+                          "(v_mfma_f32_4x4x4_16b_bf16); the line's value is the default path, v_dot2"}
+        log(f"sweep on the matrix cores (policy 'matrix'): {ms_mx * 1e3:.1f} us, {matrix['value']:.0f} GB/s compressed")
     ms_u = time_graph(sweep_ungrouped, args.steps, args.warmup)
     log(f"sweep ungrouped ({len(tensors)} launches): {ms_u * 1e3:.1f} us, "
         f"{total_bytes / (ms_u * 1e-3) / 1e9:.0f} GB/s compressed")
@@ -471,6 +487,7 @@ def main() -> int:
                               "calls": "one RadixCompressedLinear call per Linear on x [1, M, C], q/k/v and gate/up "
                                        "joined by swap.SharedInputGroup, eager, no graph"},
             "timing": "HIP graph of the sweep, replayed; events around the timed replays",
+            **({"matrix_cores": matrix} if matrix else {}),
             "weights_rng": f"dmx_synth_bf16 seed {synth.SEED}, one stream per (workload, layer, tensor)",
         },
         "roofline": {

@@ -16,6 +16,7 @@ DMX_BF16 = 0
 DMX_F32 = 1
 POLICY_AUTO = 0
 POLICY_GENERIC = 1
+POLICY_MATRIX = 2  # AUTO, with gulp's 3- and 4-row verify on the matrix cores
 
 
 class RadixTensor(ct.Structure):

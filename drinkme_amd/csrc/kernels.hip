@@ -738,14 +738,18 @@ __device__ __forceinline__ void sip_table(uint2* tb, const uint32_t* palette) {
 // decode only: each block's bf16 bits stored to the tensor's output
 // (row-major [rows, cols]) in place of the products.
 constexpr int kModeGemv = 0, kModeTwinSip = 1, kModeTwinGulp = 2, kModeDecode = 3;
+constexpr int kModeTwinGulpMx = 4;  // the raw twin of gulp under the matrix policy
 
 template <bool TWO, int M, bool PH, int MODE = kModeGemv>
-__global__ __launch_bounds__(kSipThreads, (M == 8 || (M == 4 && (MODE == kModeTwinGulp ? gulp_quad(4) : (PH || sip_quad(4))))) ? 3 : 6)
+__global__ __launch_bounds__(kSipThreads, (M == 8 || (M == 4 && (MODE == kModeTwinGulp ? gulp_quad(4) : MODE == kModeTwinGulpMx ? gulp_quad(4, true) : (PH || sip_quad(4))))) ? 3 : 6)
 void k_gemv_sip(const SipGroup g, const uint16_t* __restrict__ x, const SipShape sh) {
-    constexpr bool RAW = MODE == kModeTwinSip || MODE == kModeTwinGulp, DEC = MODE == kModeDecode;
+    constexpr bool RAW = MODE == kModeTwinSip || MODE == kModeTwinGulp || MODE == kModeTwinGulpMx;
+    constexpr bool DEC = MODE == kModeDecode;
     // verify rows four output rows at a time on the matrix cores (a raw twin
     // mirroring gulp: gulp's rule)
-    constexpr bool QUAD = !DEC && (MODE == kModeTwinGulp ? gulp_quad(M) : sip_quad(M));
+    constexpr bool QUAD = !DEC && (MODE == kModeTwinGulp    ? gulp_quad(M)
+                                   : MODE == kModeTwinGulpMx ? gulp_quad(M, true)
+                                                             : sip_quad(M));
     static_assert(!(TWO && MODE), "the raw twin and the decode run one tensor");
     static_assert(!DEC || (M == 1 && !PH), "the decode runs unphased");
     // fixed-size tables in static LDS (their addresses fold into the LDS
@@ -1390,14 +1394,15 @@ __device__ __forceinline__ void gulp_tables(uint4* t0tab, uint2* t1tab, uint8_t*
 // DEC: decode only, each block's bf16 bits stored to the tensor's output
 // (row-major [rows, cols]) in place of the products.
 // WV: waves per workgroup, the plan's (12, or 8 at three workgroups per CU).
-template <int M, bool PH, bool DEC = false, int WV = kSipWaves>
-__global__ __launch_bounds__(WV * 64, (M == 8 || (M == 4 && gulp_quad(4))) ? 3 : 6)
+// MX: the matrix policy (M = 4 in quad units, as M = 8).
+template <int M, bool PH, bool DEC = false, int WV = kSipWaves, bool MX = false>
+__global__ __launch_bounds__(WV * 64, (M == 8 || (M == 4 && gulp_quad(4, MX))) ? 3 : 6)
 void k_gemv_gulp(const SipGroup g, const uint16_t* __restrict__ x, const SipShape sh) {
     static_assert(!DEC || (M == 1 && !PH), "the decode runs unphased");
-    static_assert(WV == kSipWaves || (!PH && !DEC && !gulp_quad(M)), "8-wave workgroups run unphased v_dot2 rows");
+    static_assert(WV == kSipWaves || (!PH && !DEC && !gulp_quad(M, MX)), "8-wave workgroups run unphased v_dot2 rows");
     constexpr uint32_t W = WV, TH = 64u * WV;
     // verify rows four output rows at a time on the matrix cores
-    constexpr bool QUAD = !DEC && gulp_quad(M);
+    constexpr bool QUAD = !DEC && gulp_quad(M, MX);
     __shared__ uint4 t0tab[256];
     __shared__ uint2 t1tab[kGulpT1Entries];
     __shared__ uint2 sel2[13 * 16];
@@ -1995,6 +2000,14 @@ int raise_lds_limit(LdsFamily family, const void* const* kerns, int nk, size_t l
 
 std::atomic<int> g_policy{DMX_POLICY_AUTO};
 
+// The specialised kernels run under AUTO and MATRIX; MATRIX also puts
+// gulp's 4-row verify in quad units.
+bool fast_policy() {
+    const int p = g_policy.load();
+    return p == DMX_POLICY_AUTO || p == DMX_POLICY_MATRIX;
+}
+bool matrix_policy() { return g_policy.load() == DMX_POLICY_MATRIX; }
+
 uint64_t pad_words_for(uint32_t block, const uint32_t* w, uint32_t nw) {
     if (nw < 2 || nw > 8 || w[nw - 1] != 8) return 0;
     uint64_t most = (uint64_t(block) * 8 + 31) / 32;
@@ -2066,7 +2079,7 @@ int cu_count() {
 
 // Whether the sip kernel takes tensor t with this activation.
 bool sip_eligible(const dmx_radix_tensor* t, const void* x, int x_dtype, uint32_t m) {
-    return g_policy.load() == DMX_POLICY_AUTO && m >= 1 && m <= 8 && x_dtype == DMX_BF16 && is_sip(t) &&
+    return fast_policy() && m >= 1 && m <= 8 && x_dtype == DMX_BF16 && is_sip(t) &&
            t->block_size == 1024 &&
            t->cols % 1024 == 0 && (reinterpret_cast<uintptr_t>(x) & 15u) == 0;
 }
@@ -2154,20 +2167,24 @@ bool is_gulp(const dmx_radix_tensor* t) {
 }
 
 bool gulp_eligible(const dmx_radix_tensor* t, const void* x, int x_dtype, uint32_t m) {
-    return g_policy.load() == DMX_POLICY_AUTO && m >= 1 && m <= 8 && x_dtype == DMX_BF16 && is_gulp(t) &&
+    return fast_policy() && m >= 1 && m <= 8 && x_dtype == DMX_BF16 && is_gulp(t) &&
            t->block_size == 1024 && t->cols % 1024 == 0 && (reinterpret_cast<uintptr_t>(x) & 15u) == 0;
 }
 
 typedef void (*GulpKernel)(const SipGroup, const uint16_t*, const SipShape);
 
-// waves: the plan's waves per workgroup (8 only unphased, M <= 4)
-GulpKernel gulp_kernel(bool phased, int mi, uint32_t waves = kSipWaves) {
+// waves: the plan's waves per workgroup (8 only unphased, M <= 4);
+// matrix: the matrix policy's M = 4 (quad units)
+GulpKernel gulp_kernel(bool phased, int mi, uint32_t waves = kSipWaves, bool matrix = false) {
     static const GulpKernel table[2][4] = {
         {k_gemv_gulp<1, false>, k_gemv_gulp<2, false>, k_gemv_gulp<4, false>, k_gemv_gulp<8, false>},
         {k_gemv_gulp<1, true>, k_gemv_gulp<2, true>, k_gemv_gulp<4, true>, k_gemv_gulp<8, true>}};
     static const GulpKernel table8[3] = {k_gemv_gulp<1, false, false, kGulpWaves3>,
                                          k_gemv_gulp<2, false, false, kGulpWaves3>,
                                          k_gemv_gulp<4, false, false, kGulpWaves3>};
+    static const GulpKernel matrix4[2] = {k_gemv_gulp<4, false, false, kSipWaves, true>,
+                                          k_gemv_gulp<4, true, false, kSipWaves, true>};
+    if (matrix && mi == 2) return matrix4[phased ? 1 : 0];
     return waves == kGulpWaves3 && !phased && mi < 3 ? table8[mi] : table[phased ? 1 : 0][mi];
 }
 
@@ -2212,17 +2229,19 @@ int launch_gulp(const dmx_radix_tensor* const* ts, uint32_t n, const void* x, ui
     uint32_t grid = 0;
     size_t lds = 0;
     bool two = false;
-    if (!plan_gulp(sh, g.row0, n, min_rows, M, (uint32_t)cu_count(), grid, lds, two)) return 2;
+    const bool matrix = matrix_policy() && mi == 2;
+    if (!plan_gulp(sh, g.row0, n, min_rows, M, (uint32_t)cu_count(), grid, lds, two, matrix)) return 2;
     {
-        const void* kerns[11];
+        const void* kerns[13];
         for (int t = 0; t < 2; ++t)
             for (int i = 0; i < 4; ++i) kerns[4 * t + i] = reinterpret_cast<const void*>(gulp_kernel(t, i));
         for (int i = 0; i < 3; ++i) kerns[8 + i] = reinterpret_cast<const void*>(gulp_kernel(false, i, kGulpWaves3));
-        if (raise_lds_limit(kFamGulp, kerns, 11, lds, 64 * 1024 - fixed, "gulp kernel LDS opt-in", err, errn)) return 1;
+        for (int t = 0; t < 2; ++t) kerns[11 + t] = reinterpret_cast<const void*>(gulp_kernel(t, 2, kSipWaves, true));
+        if (raise_lds_limit(kFamGulp, kerns, 13, lds, 64 * 1024 - fixed, "gulp kernel LDS opt-in", err, errn)) return 1;
     }
-    if (sh.waves != kSipWaves && (sh.waves != kGulpWaves3 || sh.phases > 1 || mi == 3)) return 2;
-    hipLaunchKernelGGL(gulp_kernel(sh.phases > 1, mi, sh.waves), dim3(grid), dim3(64u * sh.waves), lds, stream, g,
-                       static_cast<const uint16_t*>(x), sh);
+    if (sh.waves != kSipWaves && (sh.waves != kGulpWaves3 || sh.phases > 1 || mi == 3 || matrix)) return 2;
+    hipLaunchKernelGGL(gulp_kernel(sh.phases > 1, mi, sh.waves, matrix), dim3(grid), dim3(64u * sh.waves), lds, stream,
+                       g, static_cast<const uint16_t*>(x), sh);
     return launch_check(err, errn, "gulp gemv launch");
 }
 
@@ -2287,7 +2306,7 @@ extern "C" uint64_t dmx_radix_pad_words(uint32_t block_size, const uint32_t* wid
 }
 
 extern "C" int dmx_radix_set_policy(int policy) {
-    if (policy != DMX_POLICY_AUTO && policy != DMX_POLICY_GENERIC) return -1;
+    if (policy != DMX_POLICY_AUTO && policy != DMX_POLICY_GENERIC && policy != DMX_POLICY_MATRIX) return -1;
     return g_policy.exchange(policy);
 }
 
@@ -2298,7 +2317,7 @@ extern "C" int dmx_radix_set_policy(int policy) {
 int launch_decode_fast(const dmx_radix_tensor* t, uint16_t* out, hipStream_t stream, char* err, size_t errn) {
     const bool sip = is_sip(t);
     const bool gulp = is_gulp(t);
-    if (g_policy.load() != DMX_POLICY_AUTO || !(sip || gulp) || t->block_size != 1024 || t->cols % 1024 != 0 ||
+    if (!fast_policy() || !(sip || gulp) || t->block_size != 1024 || t->cols % 1024 != 0 ||
         (reinterpret_cast<uintptr_t>(out) & 15u) != 0 || !fast_directory(t))
         return 2;
     SipGroup g;
@@ -2441,16 +2460,19 @@ typedef void (*RawKernel)(const SipGroup, const uint16_t*, const SipShape);
 // the matrix cores; gulp: v_dot2 at M = 4, quad units with gulp's tiles at
 // M = 8). At M = 1 and 2 the sip and gulp kernels do the same arithmetic,
 // so one instantiation mirrors both.
-constexpr int kRawKinds = 6;
+constexpr int kRawKinds = 7;
 RawKernel raw_kernel(bool phased, int kind) {
     static const RawKernel table[2][kRawKinds] = {
         {k_gemv_sip<false, 1, false, 1>, k_gemv_sip<false, 2, false, 1>, k_gemv_sip<false, 4, false, 1>,
-         k_gemv_sip<false, 8, false, 1>, k_gemv_sip<false, 4, false, 2>, k_gemv_sip<false, 8, false, 2>},
+         k_gemv_sip<false, 8, false, 1>, k_gemv_sip<false, 4, false, 2>, k_gemv_sip<false, 8, false, 2>,
+         k_gemv_sip<false, 4, false, kModeTwinGulpMx>},
         {k_gemv_sip<false, 1, true, 1>, k_gemv_sip<false, 2, true, 1>, k_gemv_sip<false, 4, true, 1>,
-         k_gemv_sip<false, 8, true, 1>, k_gemv_sip<false, 4, true, 2>, k_gemv_sip<false, 8, true, 2>}};
+         k_gemv_sip<false, 8, true, 1>, k_gemv_sip<false, 4, true, 2>, k_gemv_sip<false, 8, true, 2>,
+         k_gemv_sip<false, 4, true, kModeTwinGulpMx>}};
     return table[phased ? 1 : 0][kind];
 }
-int raw_kind(int mi, bool gulp) { return gulp && mi >= 2 ? 2 + mi : mi; }
+// (gulp's twin at M = 4 under the matrix policy: quad units, kind 6)
+int raw_kind(int mi, bool gulp, bool matrix) { return gulp && matrix && mi == 2 ? 6 : gulp && mi >= 2 ? 2 + mi : mi; }
 
 // The twin over the fast kernels' work split: the plan the mirrored kernel
 // (sip, or gulp with `gulp`) makes for a tensor of this shape (its static
@@ -2483,13 +2505,13 @@ int launch_raw(const uint16_t* w, uint32_t rows, uint32_t cols, bool gulp, const
     sh.bias_dtype = bias_dtype;
     sh.out_dtype = out_dtype;
     const size_t fixed = gulp ? kGulpStaticLds : kSipStaticLds;
+    const bool matrix = gulp && matrix_policy() && mi == 2;
     uint32_t grid = 0;
     size_t lds = 0;
     bool two = false;
-    if (!plan_launch(sh, g.row0, 1, rows, M, kSipWaves, gulp ? gulp_per_cu((int)M) : kSipPerCu,
-                     gulp ? gulp_quad((int)M) : sip_quad((int)M), unit_end_cost(gulp, (int)M, false), fixed,
-                     !gulp, (uint32_t)cu_count(), grid, lds,
-                     two))
+    if (!plan_launch(sh, g.row0, 1, rows, M, kSipWaves, gulp ? gulp_per_cu((int)M, matrix) : kSipPerCu,
+                     gulp ? gulp_quad((int)M, matrix) : sip_quad((int)M), unit_end_cost(gulp, (int)M, false, matrix),
+                     fixed, !gulp, (uint32_t)cu_count(), grid, lds, two))
         return 2;
     if ((uint64_t)sh.rows_per_wg * cols * 2 >= (1ull << 31)) return 2;  // a tile's bytes within the buffer range
     {
@@ -2500,8 +2522,8 @@ int launch_raw(const uint16_t* w, uint32_t rows, uint32_t cols, bool gulp, const
                             errn))
             return 1;
     }
-    hipLaunchKernelGGL(raw_kernel(sh.phases > 1, raw_kind(mi, gulp)), dim3(grid), dim3(kSipThreads), lds, stream, g,
-                       static_cast<const uint16_t*>(x), sh);
+    hipLaunchKernelGGL(raw_kernel(sh.phases > 1, raw_kind(mi, gulp, matrix)), dim3(grid), dim3(kSipThreads), lds, stream,
+                       g, static_cast<const uint16_t*>(x), sh);
     return launch_check(err, errn, "raw twin gemv launch");
 }
 
@@ -2525,7 +2547,7 @@ extern "C" int dmx_radix_gemv_twin(const uint16_t* w, uint32_t rows, uint32_t co
     t.block_size = block_size;
     t.n_widths = n_widths;
     for (uint32_t j = 0; j < n_widths; ++j) t.widths[j] = widths[j];
-    const bool fast = g_policy.load() == DMX_POLICY_AUTO && m >= 1 && m <= 8 && x_dtype == DMX_BF16 &&
+    const bool fast = fast_policy() && m >= 1 && m <= 8 && x_dtype == DMX_BF16 &&
                       block_size == 1024 && cols % 1024 == 0 && (reinterpret_cast<uintptr_t>(x) & 15u) == 0 &&
                       (reinterpret_cast<uintptr_t>(w) & 15u) == 0;
     if (fast && (is_sip(&t) || is_gulp(&t))) {

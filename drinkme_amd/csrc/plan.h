@@ -144,9 +144,11 @@ constexpr size_t kGulpStaticLds = kGulpT0Bytes + ((kGulpT1Entries * 8 + 15) & ~1
 // per CU; gulp's decode is bound by latency and wants the waves of two, so
 // at M = 4 it keeps v_dot2 (the quad path measured 4-13% slower there on
 // Qwen3-8B and 32B-class layers, and 4-8% faster at M = 8).
+// The matrix policy (DMX_POLICY_MATRIX) also puts gulp's 4-row verify in
+// quad units, so that path can be chosen and measured.
 DMX_HD constexpr bool sip_quad(int M) { return M >= 4; }
-DMX_HD constexpr bool gulp_quad(int M) { return M >= 8; }
-DMX_HD constexpr uint32_t gulp_per_cu(int M) { return gulp_quad(M) ? 1u : kGulpPerCu; }
+DMX_HD constexpr bool gulp_quad(int M, bool matrix = false) { return M >= 8 || (matrix && M == 4); }
+DMX_HD constexpr uint32_t gulp_per_cu(int M, bool matrix = false) { return gulp_quad(M, matrix) ? 1u : kGulpPerCu; }
 
 struct SipShape {
     uint32_t rows, cols, nb;  // rows of the whole group
@@ -418,8 +420,8 @@ DMX_HD GulpLanes gulp_lanes(uint32_t lane) {
 // layer 1.1-1.4% faster at M = 1 and 1.0-2.1% at M = 4, the 32B-class
 // layer 0.5-1.9% at M = 1, over two A/B runs); charging the quad units so
 // made M = 8 9% slower.
-DMX_HD constexpr double unit_end_cost(bool gulp, int M, bool decode) {
-    return gulp && !decode && !gulp_quad(M) ? 1.0 : 0.25;
+DMX_HD constexpr double unit_end_cost(bool gulp, int M, bool decode, bool matrix = false) {
+    return gulp && !decode && !gulp_quad(M, matrix) ? 1.0 : 0.25;
 }
 
 // The work plan of a sip or gulp launch over the group's sh.rows rows (row0:
@@ -542,12 +544,13 @@ inline bool plan_launch(SipShape& sh, const uint32_t* row0, uint32_t n, uint32_t
 // CU, at most three) run 8-wave workgroups, three per CU, all resident at
 // once.
 inline bool plan_gulp(SipShape& sh, const uint32_t* row0, uint32_t n, uint32_t min_rows, uint32_t M, uint32_t cus,
-                      uint32_t& grid_out, size_t& lds_out, bool& two_out) {
-    const double uc = unit_end_cost(true, (int)M, false);
-    if (!plan_launch(sh, row0, n, min_rows, M, kPlanWaves, gulp_per_cu((int)M), gulp_quad((int)M), uc, kGulpStaticLds,
+                      uint32_t& grid_out, size_t& lds_out, bool& two_out, bool matrix = false) {
+    const bool quad = gulp_quad((int)M, matrix);
+    const double uc = unit_end_cost(true, (int)M, false, matrix);
+    if (!plan_launch(sh, row0, n, min_rows, M, kPlanWaves, gulp_per_cu((int)M, matrix), quad, uc, kGulpStaticLds,
                      false, cus, grid_out, lds_out, two_out))
         return false;
-    if (!gulp_quad((int)M) && grid_out > 2 * cus && grid_out <= 3 * cus) {
+    if (!quad && grid_out > 2 * cus && grid_out <= 3 * cus) {
         SipShape s3 = sh;
         uint32_t g3 = 0;
         size_t l3 = 0;

@@ -442,9 +442,14 @@ def read_bytes(p: dict) -> int:
     return words * 4 + sum(p[k].numel() * p[k].element_size() for k in ("rx_offsets", "rx_palette", "rx_schedule"))
 
 
+_POLICIES = {"auto": _native.POLICY_AUTO, "generic": _native.POLICY_GENERIC, "matrix": _native.POLICY_MATRIX}
+
+
 def set_policy(policy: str) -> str:
-    """'auto' (specialised kernels where they apply) or 'generic'; returns
-    the previous one."""
-    code = {"auto": _native.POLICY_AUTO, "generic": _native.POLICY_GENERIC}[policy]
+    """'auto' (specialised kernels where they apply), 'generic', or
+    'matrix' (auto's kernels with gulp's 3- and 4-row verify in quad units
+    on the matrix cores, as 8 rows run; no drinkme counterpart); returns the
+    previous one. Process-global."""
+    code = _POLICIES[policy]
     prev = _native.lib().dmx_radix_set_policy(code)
-    return {_native.POLICY_AUTO: "auto", _native.POLICY_GENERIC: "generic"}[prev]
+    return {v: k for k, v in _POLICIES.items()}[prev]

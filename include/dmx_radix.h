@@ -47,6 +47,7 @@ extern "C" {
 /* dmx_radix_set_policy */
 #define DMX_POLICY_AUTO 0    /* the specialised kernels where they apply */
 #define DMX_POLICY_GENERIC 1 /* the generic decoder for every tensor */
+#define DMX_POLICY_MATRIX 2  /* as AUTO, with gulp's 3- and 4-row verify on the matrix cores too */
 
 /* One radix tensor resident on the device: the runtime dict of
  * swap.to_device_radix (src/drinkme/codec/swap.py:80-161) as plain
@@ -208,8 +209,12 @@ int dmx_pack_read(const char* path, const char* name, dmx_pack_info* info, uint8
 int dmx_pack_write(const char* path, const dmx_pack_info* info, const uint8_t* palette, const uint32_t* offsets,
                    const uint32_t* data, const uint16_t* raw_bits, char* err, size_t errn);
 
-/* Kernel choice for dmx_radix_gemv: DMX_POLICY_AUTO or DMX_POLICY_GENERIC
- * (an A/B switch like DRINKME_RADIX_DECODER, radix_ops.py:286-300).
+/* Kernel choice for dmx_radix_gemv: DMX_POLICY_AUTO, DMX_POLICY_GENERIC
+ * (an A/B switch like DRINKME_RADIX_DECODER, radix_ops.py:286-300) or
+ * DMX_POLICY_MATRIX (AUTO's kernels, gulp's M = 3..4 verify rows in quad
+ * units on the matrix cores, as M = 8 runs; AUTO keeps them on v_dot2,
+ * measured faster there; the raw twin follows). No drinkme counterpart for
+ * MATRIX: drinkme has one verify path. Process-global.
  * Returns the previous policy, or -1 for an unknown one. */
 int dmx_radix_set_policy(int policy);
 

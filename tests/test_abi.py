@@ -50,7 +50,8 @@ def test_calls_that_need_no_gpu():
 
     L = _native.lib()
     assert L.dmx_radix_set_policy(1) in (0, 1)
-    assert L.dmx_radix_set_policy(0) == 1
+    assert L.dmx_radix_set_policy(2) == 1
+    assert L.dmx_radix_set_policy(0) == 2
     assert L.dmx_radix_set_policy(7) < 0
     err = _native.error_buffer()
     w = np.array([3, 8], np.uint32)

@@ -199,8 +199,9 @@ def kernel_asm(tmp_path_factory):
 def test_every_sip_and_gulp_kernel_keeps_its_inflight_registers(kernel_asm):
     ks = kernels(kernel_asm, r"k_gemv_(sip|gulp)I")
     # sip: 3 kinds x M = 1, 2, 4, 8; gulp: 2 x 4, and 8-wave workgroups at M = 1, 2, 4; the raw twin:
-    # 2 x (M = 1, 2, 4, 8, and M = 4, 8 as gulp); the decode: sip and gulp
-    assert len(ks) == 37
+    # 2 x (M = 1, 2, 4, 8, and M = 4, 8 as gulp); the decode: sip and gulp; the matrix policy's gulp
+    # M = 4 in quad units and its twin, unphased and phased
+    assert len(ks) == 41
     for name, body in ks.items():
         hazards, reached, total = analyse(body)
         assert reached == total, f"{name}: walked {reached} of {total} blocks"
@@ -266,10 +267,10 @@ def test_static_lds_fits_what_the_plans_reserve(kernel_asm, tmp_path):
         if fam is None:
             continue
         seen += 1
-        # the raw twin mirroring gulp (k_gemv_sip<false, M, PH, 2>) runs gulp's plan; at M = 1, 2 the
-        # twins of both run k_gemv_sip<false, M, PH, 1> under either plan
-        twin = re.search(r"k_gemv_sipILb0ELi(\d)ELb[01]ELi([12])E", name)
-        gulp_plan = fam == "gulp" or (twin and (twin.group(2) == "2" or twin.group(1) in "12"))
+        # the raw twins mirroring gulp (k_gemv_sip<false, M, PH, 2>, and 4 under the matrix policy) run
+        # gulp's plan; at M = 1, 2 the twins of both run k_gemv_sip<false, M, PH, 1> under either plan
+        twin = re.search(r"k_gemv_sipILb0ELi(\d)ELb[01]ELi([124])E", name)
+        gulp_plan = fam == "gulp" or (twin and (twin.group(2) in "24" or twin.group(1) in "12"))
         limit = gulp_lds if gulp_plan else sip_lds
         assert fields["group_segment_fixed_size"] <= limit, (name, fields["group_segment_fixed_size"], limit)
-    assert seen == 37
+    assert seen == 41

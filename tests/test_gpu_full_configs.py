@@ -5,8 +5,9 @@ gate/up of a layer as one launch each, o and down alone).
   - the single 4096 x 4096 linear, N(0, 0.02), sip, M = 1;
   - Qwen3-8B layer (4096 hidden; q 4096x4096, k/v 1024x4096, o 4096x4096,
     gate/up 12288x4096, down 4096x12288), N(0, 0.02), sip, M = 1;
-  - the same layer at gulp, M = 4 (the MTP verify rows), and at sip, M = 4
-    (its blocks contracted on the matrix cores);
+  - the same layer at gulp, M = 4 (the MTP verify rows), also under the
+    matrix policy (gulp's verify rows in quad units on the matrix cores),
+    and at sip, M = 4 (its blocks contracted on the matrix cores);
   - the Qwen3-8B lm_head, 151936 x 4096 N(0, 0.02), sip, M = 1: the largest
     launch of the decode-step sweep, with its own plan (about 2,400 blocks
     per CU, progress balance on);
@@ -134,6 +135,18 @@ def test_qwen3_8b_layer_gulp_m4(cuda):
     from drinkme_amd import synth
 
     _layer(cuda, "qwen3-8b", 0, synth.QWEN3_8B_LAYER, synth.NORMAL, "gulp", 4, "qwen3-8b-layer")
+
+
+def test_qwen3_8b_layer_gulp_m4_matrix_cores(cuda):
+    """The same C3 layer under the matrix policy: gulp's four verify rows in
+    quad units on the matrix cores (AUTO keeps them on v_dot2)."""
+    from drinkme_amd import radix_ops, synth
+
+    prev = radix_ops.set_policy("matrix")
+    try:
+        _layer(cuda, "qwen3-8b", 0, synth.QWEN3_8B_LAYER, synth.NORMAL, "gulp", 4, "qwen3-8b-layer")
+    finally:
+        radix_ops.set_policy(prev)
 
 
 def test_qwen3_8b_layer_sip_m4(cuda):

@@ -42,9 +42,11 @@ void bad(const std::string& what) {
     ++g_bad;
 }
 
-enum Kind { kSip, kGulp, kDecodeSip, kDecodeGulp, kTwinSip, kTwinGulp };
+// kGulpMatrix / kTwinGulpMatrix: gulp and its twin under the matrix policy
+enum Kind { kSip, kGulp, kDecodeSip, kDecodeGulp, kTwinSip, kTwinGulp, kGulpMatrix, kTwinGulpMatrix };
 const char* kind_name(Kind k) {
-    static const char* n[] = {"sip", "gulp", "decode-sip", "decode-gulp", "twin-sip", "twin-gulp"};
+    static const char* n[] = {"sip",      "gulp",      "decode-sip",  "decode-gulp",
+                              "twin-sip", "twin-gulp", "gulp-matrix", "twin-gulp-matrix"};
     return n[k];
 }
 
@@ -70,12 +72,13 @@ struct Launch {
 
 Launch launch_of(Kind k, uint32_t M) {
     Launch l{};
-    l.gulp = k == kGulp || k == kDecodeGulp || k == kTwinGulp;
+    const bool matrix = k == kGulpMatrix || k == kTwinGulpMatrix;
+    l.gulp = k == kGulp || k == kDecodeGulp || k == kTwinGulp || matrix;
     const bool dec = k == kDecodeSip || k == kDecodeGulp;
-    l.per_cu = dec ? kDecodePerCu : l.gulp ? gulp_per_cu((int)M) : kSipPerCu;
-    l.quad = dec ? false : l.gulp ? gulp_quad((int)M) : sip_quad((int)M);
+    l.per_cu = dec ? kDecodePerCu : l.gulp ? gulp_per_cu((int)M, matrix) : kSipPerCu;
+    l.quad = dec ? false : l.gulp ? gulp_quad((int)M, matrix) : sip_quad((int)M);
     l.allow_two = !l.gulp;
-    l.unit_cost = unit_end_cost(l.gulp, (int)M, dec);
+    l.unit_cost = unit_end_cost(l.gulp, (int)M, dec, matrix);
     l.fixed = l.gulp ? kGulpStaticLds : kSipStaticLds;
     return l;
 }
@@ -201,7 +204,8 @@ void run(const Case& cs) {
     size_t lds = 0;
     bool two = false;
     // (the gulp GEMV plans through plan_gulp, as its launcher does)
-    if (cs.kind == kGulp ? !plan_gulp(sh, row0, n, min_rows, M, cs.cus, grid, lds, two)
+    if (cs.kind == kGulp || cs.kind == kGulpMatrix
+            ? !plan_gulp(sh, row0, n, min_rows, M, cs.cus, grid, lds, two, cs.kind == kGulpMatrix)
                          : !plan_launch(sh, row0, n, min_rows, M, kPlanWaves, l.per_cu, l.quad, l.unit_cost, l.fixed,
                                         l.allow_two, cs.cus, grid, lds, two))
         return;  // the generic kernel runs
@@ -212,7 +216,8 @@ void run(const Case& cs) {
     if ((lds + l.fixed) > kLdsBytes) bad(tag + ": LDS past the CU's");
     if (sh.segs * sh.seg_blocks != sh.nb || sh.phases * sh.phase_blocks != sh.nb) bad(tag + ": segments do not tile the row");
     if (sh.quad && sh.rows_per_wg % 4) bad(tag + ": a quad tile of " + std::to_string(sh.rows_per_wg) + " rows");
-    if ((cs.kind == kTwinSip || cs.kind == kTwinGulp) && (uint64_t)sh.rows_per_wg * cs.cols * 2 >= (1ull << 31))
+    if ((cs.kind == kTwinSip || cs.kind == kTwinGulp || cs.kind == kTwinGulpMatrix) &&
+        (uint64_t)sh.rows_per_wg * cs.cols * 2 >= (1ull << 31))
         return;  // the host refuses the fast twin
     if (two)
         walk_launch<true>(cs, sh, row0, grid);
@@ -337,12 +342,13 @@ int main(int argc, char** argv) {
         {{151936}, 4096},       {{8192, 1024, 1024}, 5120}, {{5120}, 8192},          {{25600, 25600}, 5120},
         {{5120}, 25600},        {{1024}, 4096},             {{1}, 1024},             {{3, 5, 7, 9}, 2048},
         {{1000, 24, 3000}, 3072}};
-    const Kind kinds[] = {kSip, kGulp, kDecodeSip, kDecodeGulp, kTwinSip, kTwinGulp};
+    const Kind kinds[] = {kSip, kGulp, kDecodeSip, kDecodeGulp, kTwinSip, kTwinGulp, kGulpMatrix, kTwinGulpMatrix};
     for (const auto& s : shapes)
         for (Kind k : kinds)
             for (uint32_t m : {1u, 2u, 3u, 4u, 5u, 8u})
                 for (uint32_t cus : {256u, 80u, 7u}) {
-                    if ((k == kDecodeSip || k == kDecodeGulp || k == kTwinSip || k == kTwinGulp) &&
+                    if ((k == kDecodeSip || k == kDecodeGulp || k == kTwinSip || k == kTwinGulp ||
+                         k == kTwinGulpMatrix) &&
                         (s.first.size() > 1 || ((k == kDecodeSip || k == kDecodeGulp) && m > 1)))
                         continue;
                     run(Case{k, s.first, s.second, m, cus});
@@ -350,7 +356,7 @@ int main(int argc, char** argv) {
     // seeded random groups
     for (int i = 0; i < 600; ++i) {
         Case c;
-        const Kind k = kinds[rnd(2)];
+        const Kind k = i % 3 == 2 ? kGulpMatrix : kinds[rnd(2)];
         c.kind = k;
         const uint32_t n = 1 + rnd(4);
         for (uint32_t j = 0; j < n; ++j) c.rows.push_back(rnd(4) == 0 ? 1 + rnd(40) : 1 + rnd(20000));
