@@ -161,3 +161,28 @@ def test_graph_of_member_calls_replays_the_grouped_launches(cuda, profile):
         for n, o, w in zip(names, outs, want):
             assert torch.equal(o, w), f"replay {rep}: {n}"
         torch.cuda.synchronize()
+
+
+def test_inference_mode_activations_share_the_launch(cuda):
+    """Under torch.inference_mode (no version counter) the members match
+    the activation by identity: one launch, the grouped launch's rows."""
+    import torch
+
+    from drinkme_amd import radix_ops, swap
+
+    layer, bits, qb = _layer(cuda, "sip", 51)
+    swap.install_groups(layer)
+    a = layer.self_attn
+    calls = _counting(a.q_proj._group)
+    rng = np.random.default_rng(52)
+    xb = O.f32_to_bf16_bits(rng.standard_normal((1, 1, C)).astype(np.float32))
+    print("case shared-input inference mode", flush=True)
+    with torch.inference_mode():
+        x = bf16_tensor(xb, cuda).clone()
+        assert x.is_inference()
+        got = [a.q_proj(x), a.k_proj(x), a.v_proj(x)]
+        want = radix_ops.gemv_group([a.q_proj.p, a.k_proj.p, a.v_proj.p], x.reshape(1, C), [qb, None, None],
+                                    torch.bfloat16)
+    assert calls == [1]
+    for g, w in zip(got, want):
+        assert torch.equal(g.reshape(1, -1), w)
