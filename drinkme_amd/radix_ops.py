@@ -91,11 +91,12 @@ def _error_buffer():
 
 
 def _buffers(p: dict) -> tuple:
-    return p["rx_data"], p["rx_offsets"], p["rx_palette"], p.get("rx_schedule")
-
-
-def _same_buffers(a: tuple, b: tuple) -> bool:
-    return a[0] is b[0] and a[1] is b[1] and a[2] is b[2] and a[3] is b[3]
+    """The addresses of a runtime dict's buffers: a launcher's descriptor is
+    rebuilt when any of them moves (another tensor in the dict, or new
+    storage under the same tensor)."""
+    sched = p.get("rx_schedule")
+    return (p["rx_data"].data_ptr(), p["rx_offsets"].data_ptr(), p["rx_palette"].data_ptr(),
+            sched.data_ptr() if sched is not None else 0)
 
 
 def _dtype_code(dtype, what):
@@ -227,7 +228,7 @@ class RowsLauncher:
 
     def _pointer(self):
         held = _buffers(self.p)
-        if self._held is None or not _same_buffers(held, self._held):
+        if held != self._held:
             self._ptr = ct.pointer(descriptor(self.p))
             self._held = held
         return self._ptr
@@ -310,7 +311,7 @@ class GroupLauncher:
         """The descriptor pointer array, rebuilt when a dict's buffers are no
         longer the ones it was built from."""
         held = [_buffers(p) for p in self.ps]
-        if self._held is None or not all(_same_buffers(a, b) for a, b in zip(held, self._held)):
+        if held != self._held:
             descs = [descriptor(p) for p in self.ps]
             self._tarr = (ct.POINTER(_native.RadixTensor) * len(descs))(*[ct.pointer(d) for d in descs])
             self._descs = descs  # the array points into these
@@ -319,10 +320,9 @@ class GroupLauncher:
 
     def _bias_array(self, biases, x):
         """(pointer array, dtype code, the biases it points into); kept while
-        the same contiguous bias tensors come back."""
-        key = tuple(biases)
-        if self._bias_key is not None and len(key) == len(self._bias_key) and \
-                all(a is b for a, b in zip(key, self._bias_key)):
+        the same contiguous bias tensors come back at the same addresses."""
+        key = tuple(None if b is None else (b.data_ptr(), b.dtype, b.numel()) for b in biases)
+        if key == self._bias_key:
             return self._bias_cached
         n = len(self.ps)
         if len(biases) != n:
@@ -336,7 +336,9 @@ class GroupLauncher:
                 raise ValueError("radix gemv_group: bias must hold R elements on the weight's device")
         bd = _dtype_code(dts.pop(), "bias") if dts else 0
         cached = (ct.c_void_p * n)(*[None if b is None else b.data_ptr() for b in biases]), bd, biases
-        if all(b is None or b is c for b, c in zip(key, biases)):  # (no copies made: the same tensors next time)
+        # (kept only when no copy was made: the array then points into the
+        # callers' own tensors, which the key follows)
+        if all(a is None or a[0] == b.data_ptr() for a, b in zip(key, biases)):
             self._bias_key, self._bias_cached = key, cached
         return cached
 

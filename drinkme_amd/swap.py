@@ -307,9 +307,10 @@ class SharedInputGroup:
     The first member called with an activation launches the GEMVs of every
     member and keeps the other members' rows; a member called next with
     that same activation takes its rows from the launch. "That same
-    activation" means the same tensor object, with torch's version counter
-    unchanged since the launch (no in-place write through torch), the same
-    row count, on the same stream and under the same graph-capture state.
+    activation" means the same tensor object, at the same address and of the
+    same dtype, with torch's version counter unchanged since the launch (no
+    in-place write through torch), the same row count, on the same stream
+    and under the same graph-capture state.
     The group holds the activation until every member has taken its rows,
     so its memory cannot pass to another tensor meanwhile. Anything else (a
     member called twice, another activation, an in-place write) launches
@@ -350,7 +351,7 @@ class SharedInputGroup:
     @staticmethod
     def _match(x, m: int):
         version = None if x.is_inference() else x._version
-        return (m, version, radix_ops._stream(x.device), torch.cuda.is_current_stream_capturing())
+        return (m, x.data_ptr(), x.dtype, version, radix_ops._stream(x.device), torch.cuda.is_current_stream_capturing())
 
     def rows(self, slot: int, x: torch.Tensor) -> torch.Tensor:
         """Member `slot`'s rows of activation x [..., C]: [..., R] in x's

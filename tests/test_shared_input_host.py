@@ -192,3 +192,30 @@ def test_the_launch_gets_the_members_biases_and_x_dtype(monkeypatch):
     g.rows(1, x)
     (biases, dtype), = seen
     assert biases[0] is bq and biases[1] is None and dtype == torch.float32
+
+
+def test_new_storage_under_the_same_activation_launches_again(counted):
+    g, calls = counted
+    x = _x()
+    g.rows(0, x)
+    x.data = x.data.clone()  # the same object over new memory, its version untouched
+    g.rows(1, x)
+    assert len(calls) == 2
+
+
+def test_the_bias_array_follows_the_biases_addresses():
+    from drinkme_amd import radix_ops
+
+    gl = radix_ops.GroupLauncher([_fake_runtime(8, 64), _fake_runtime(4, 64)])
+    x = torch.zeros(1, 64, dtype=torch.bfloat16)
+    b = torch.ones(8, dtype=torch.bfloat16)
+    arr, bd, kept = gl._bias_array([b, None], x)
+    assert arr[0] == b.data_ptr() and arr[1] is None
+    assert gl._bias_array([b, None], x)[0] is arr, "the same biases at the same addresses: the cached array"
+    b.data = torch.full((8,), 2.0, dtype=torch.bfloat16)  # new storage under the same Parameter-like tensor
+    arr2 = gl._bias_array([b, None], x)[0]
+    assert arr2 is not arr and arr2[0] == b.data_ptr()
+    wide = torch.ones(16, dtype=torch.bfloat16)[::2]  # not contiguous: copied for the call, never cached
+    arr3, _, kept3 = gl._bias_array([wide, None], x)
+    assert arr3[0] == kept3[0].data_ptr() != wide.data_ptr()
+    assert gl._bias_array([wide, None], x)[0] is not arr3
