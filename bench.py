@@ -26,7 +26,10 @@ without a graph, the way a serving loop calls it: one radix_ops call per
 Linear (config.eager_ungrouped), and one module call per Linear with the
 q/k/v and gate/up modules in shared-input groups (config.eager_modules).
 For gulp at M = 3..4 the sweep is also timed with its verify rows on the
-matrix cores (radix_ops.set_policy("matrix"), config.matrix_cores).
+matrix cores (radix_ops.set_policy("matrix"), config.matrix_cores). The
+ceiling beside it (config.read_wall): the same launches as plain
+non-temporal reads of their bytes (dmx_read_probe), in a graph timed the
+same way, and the largest launch's bytes read alone.
 Reported:
   value       whole-sweep compressed-HBM GB/s = sum of algorithmic bytes /
               step time, B = 4 NW + 4 (R NB + 1) + P + 2 M C + 2 M R per
@@ -390,6 +393,41 @@ def main() -> int:
     value = total_bytes / (ms * 1e-3) / 1e9
     log(f"sweep ({len(groups)} launches): {ms * 1e3:.1f} us, {value:.0f} GB/s compressed ({value / PEAK_GBPS:.1%}), "
         f"{total_bf16 / (ms * 1e-3) / 1e9:.0f} GB/s bf16-equivalent")
+    # the same launches as plain reads of their bytes (dmx_read_probe, one
+    # launch per launch of the sweep, each over a buffer of its own): the
+    # ceiling for this sweep on this box, timed the same way
+    wgs = 2 * torch.cuda.get_device_properties(0).multi_processor_count
+    sink = torch.zeros(wgs, dtype=torch.int32, device="cuda")
+    rbufs = [torch.empty((b + 15) // 16 * 4, dtype=torch.int32, device="cuda") for b in gbytes]
+
+    def read_launch(buf):
+        st = lib.dmx_read_probe(buf.data_ptr(), buf.numel() * 4, sink.data_ptr(), wgs, stream(), err, len(err))
+        if st:
+            raise RuntimeError(err.value.decode())
+
+    def read_sweep():
+        for buf in rbufs:
+            read_launch(buf)
+
+    big = max(rbufs, key=lambda b: b.numel())
+
+    def read_big():
+        for _ in range(4):
+            read_launch(big)
+
+    ms_r = time_graph(read_sweep, args.steps, args.warmup)
+    read_bytes = sum(b.numel() * 4 for b in rbufs)
+    big_gbps = 4 * big.numel() * 4 / (time_graph(read_big, args.steps, args.warmup) * 1e-3) / 1e9
+    read_wall = {"us_per_sweep": round(ms_r * 1e3, 2), "value": round(read_bytes / (ms_r * 1e-3) / 1e9, 1),
+                 "pct_of_hbm_peak": round(100 * read_bytes / (ms_r * 1e-3) / 1e9 / PEAK_GBPS, 2),
+                 "sweep_fraction_of_read_wall": round(ms_r / ms, 4),
+                 "largest_launch": {"bytes": big.numel() * 4, "value": round(big_gbps, 1)},
+                 "kernel": f"dmx_read_probe: non-temporal 16-byte reads, {wgs} workgroups of 1024 threads, one launch "
+                           "per launch of the sweep over its algorithmic bytes"}
+    del rbufs, big
+    log(f"plain read of the same launches: {ms_r * 1e3:.1f} us, {read_wall['value']:.0f} GB/s "
+        f"({read_wall['pct_of_hbm_peak']:.1f}% of peak); the sweep runs at {read_wall['sweep_fraction_of_read_wall']:.1%} "
+        f"of it; the largest launch's bytes alone read at {big_gbps:.0f} GB/s")
     # gulp's 3- and 4-row verify: AUTO runs it on v_dot2 (measured faster);
     # the matrix policy runs it in quad units on the matrix cores, as 8 rows
     # run: the same sweep timed on that path too
@@ -486,6 +524,7 @@ def main() -> int:
                               "host_issue_us_per_sweep": round(host_md * 1e3, 1),
                               "calls": "one RadixCompressedLinear call per Linear on x [1, M, C], q/k/v and gate/up "
                                        "joined by swap.SharedInputGroup, eager, no graph"},
+            "read_wall": read_wall,
             "timing": "HIP graph of the sweep, replayed; events around the timed replays",
             **({"matrix_cores": matrix} if matrix else {}),
             "weights_rng": f"dmx_synth_bf16 seed {synth.SEED}, one stream per (workload, layer, tensor)",

@@ -74,6 +74,7 @@ SIGNATURES = {
     "dmx_pack_read": (_I, [ct.c_char_p, ct.c_char_p, _P, _P, _P, _P, _P, _P, _SZ]),
     "dmx_pack_write": (_I, [ct.c_char_p, _P, _P, _P, _P, _P, _P, _SZ]),
     "dmx_radix_set_policy": (_I, [_I]),
+    "dmx_read_probe": (_I, [_P, _U64, _P, _U32, _P, _P, _SZ]),
     "dmx_synth_bf16": (_I, [_U64, _U64, _U64, ct.c_double, _U32, _P, _P, _SZ]),
 }
 

@@ -1960,6 +1960,53 @@ __global__ __launch_bounds__(kNarrowThreads) void k_gemv_narrow(const uint16_t* 
     }
 }
 
+// ------------------------------------------------------ plain-read probe --
+//
+// A plain streaming read of `bytes` bytes of device memory: the ceiling a
+// decode launch of the same bytes is measured against. The range is read
+// as 1 KB rows, wave w of the grid's n taking rows w, w + n, w + 2n, ...,
+// one non-temporal 16-byte load per lane per row (the payload loads'
+// policy), one row in flight, through a buffer resource over exactly those
+// bytes (a lane past the end reads 0 and fetches nothing). Of the layouts
+// measured (rows interleaved or a contiguous run per wave; 768 or 1024
+// threads; one, two or four rows in flight; one to eight workgroups per CU)
+// this one, at two 1024-thread workgroups per CU, read the Qwen3-8B step's
+// launches and a single 0.87 GB range fastest (6.3 and 7.0 TB/s). Each
+// workgroup stores the XOR of every 32-bit word it read to
+// sink[workgroup], so the reads cannot be dropped and a test can check
+// them.
+constexpr uint32_t kProbeThreads = 1024;
+
+__global__ __launch_bounds__(kProbeThreads) void k_read_probe(const uint8_t* __restrict__ data, uint32_t bytes,
+                                                               uint32_t* __restrict__ sink) {
+    __shared__ uint32_t part[kProbeThreads / kWave];
+    const i32x4 r = make_rsrc(data, bytes);
+    const uint32_t lane = lane_id(), wv = wave_id();
+    const uint32_t nw = gridDim.x * (kProbeThreads / kWave), gw = blockIdx.x * (kProbeThreads / kWave) + wv;
+    const uint32_t rows = (bytes + 1023u) / 1024u;
+    uint32_t acc = 0;
+    for (uint32_t row = gw; row < rows; row += nw) {
+        u32x4 a;
+        asm volatile(
+            "buffer_load_dwordx4 %0, %1, %2, 0 offen nt\n\t"
+            "s_waitcnt vmcnt(0)"
+            : "=&v"(a)
+            : "v"(row * 1024u + 16u * lane), "s"(r)
+            : "memory");
+        acc ^= a.x ^ a.y ^ a.z ^ a.w;
+    }
+#pragma unroll
+    for (int k = 32; k >= 1; k >>= 1) acc ^= __shfl_xor(acc, k, kWave);
+    if (lane == 0) part[wv] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint32_t x = 0;
+#pragma unroll
+        for (uint32_t k = 0; k < kProbeThreads / kWave; ++k) x ^= part[k];
+        sink[blockIdx.x] = x;
+    }
+}
+
 // ------------------------------------------------------------- host side --
 
 int fail(char* err, size_t n, const char* msg) {
@@ -2571,4 +2618,15 @@ extern "C" int dmx_radix_gemv_twin(const uint16_t* w, uint32_t rows, uint32_t co
         default: launch_generic_m<8, true>(d, x, x_dtype, bias, bias_dtype, out, out_dtype, s); break;
     }
     return launch_check(err, errn, "raw twin generic gemv launch");
+}
+
+extern "C" int dmx_read_probe(const void* data, uint64_t bytes, uint32_t* sink, uint32_t sink_words, void* stream,
+                              char* err, size_t errn) {
+    if (!data || !sink) return fail(err, errn, "null data or sink");
+    if (bytes == 0 || bytes % 16 != 0) return fail(err, errn, "bytes must be a positive multiple of 16");
+    if (bytes >= (1ull << 31)) return fail(err, errn, "a probe reads less than 2^31 bytes");
+    if (sink_words == 0 || sink_words > 65535) return fail(err, errn, "sink_words (the workgroups) outside 1..65535");
+    hipLaunchKernelGGL(k_read_probe, dim3(sink_words), dim3(kProbeThreads), 0, static_cast<hipStream_t>(stream),
+                       static_cast<const uint8_t*>(data), (uint32_t)bytes, sink);
+    return launch_check(err, errn, "read probe launch");
 }

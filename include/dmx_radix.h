@@ -227,6 +227,16 @@ int dmx_radix_set_policy(int policy);
 int dmx_synth_bf16(uint64_t seed, uint64_t stream, uint64_t count, double scale, uint32_t dist, uint16_t* out,
                    char* err, size_t errn);
 
+/* A plain streaming read of `bytes` (a positive multiple of 16, below 2^31)
+ * of device memory at `data`, with the payload loads' non-temporal 16-byte
+ * reads: the ceiling that a decode launch of the same bytes is measured
+ * against. No drinkme counterpart: a measurement probe. sink_words
+ * workgroups of 1024 threads (1..65535) each read a contiguous share and
+ * store the XOR of the 32-bit words they read to sink[workgroup], so the
+ * XOR of sink[0 .. sink_words) is the XOR of every word of the range. */
+int dmx_read_probe(const void* data, uint64_t bytes, uint32_t* sink, uint32_t sink_words, void* stream, char* err,
+                   size_t errn);
+
 #ifdef __cplusplus
 }
 #endif

@@ -88,3 +88,27 @@ def test_group_refusals():
     st = L.dmx_radix_gemv_group(arr, 2, FAKE, _native.DMX_BF16, 1, None, 0, outs, _native.DMX_BF16, None, err,
                                 len(err))
     assert st != 0 and b"share cols" in err.value
+
+
+PROBE_CASES = [
+    ("null data", {"data": None}, b"null data or sink"),
+    ("null sink", {"sink": None}, b"null data or sink"),
+    ("no bytes", {"bytes": 0}, b"positive multiple of 16"),
+    ("ragged bytes", {"bytes": 1000}, b"positive multiple of 16"),
+    ("2^31 bytes", {"bytes": 1 << 31}, b"less than 2^31"),
+    ("no workgroups", {"sink_words": 0}, b"outside 1..65535"),
+    ("too many workgroups", {"sink_words": 65536}, b"outside 1..65535"),
+]
+
+
+@pytest.mark.parametrize("name,kw,msg", PROBE_CASES, ids=[c[0] for c in PROBE_CASES])
+def test_read_probe_refuses_before_any_device_call(name, kw, msg):
+    from drinkme_amd import _native
+
+    L = _native.lib()
+    err = _native.error_buffer()
+    a = {"data": FAKE, "bytes": 4096, "sink": FAKE, "sink_words": 512}
+    a.update(kw)
+    st = L.dmx_read_probe(a["data"], a["bytes"], a["sink"], a["sink_words"], None, err, len(err))
+    assert st != 0, f"{name}: accepted"
+    assert msg in err.value, f"{name}: {err.value!r}"

@@ -71,6 +71,11 @@ def test_the_json_line_carries_the_contract():
     assert abs(out["value"] - c["compressed_bytes"] / (out["ms_per_step"] * 1e-3) / 1e9) <= 0.01 * out["value"]
     for k in ("ungrouped", "eager_ungrouped", "eager_modules"):
         assert c[k]["us_per_sweep"] > 0 and c[k]["launches"] >= 1, k
+    # the plain read of the same launches: a ceiling for the same bytes, so
+    # no faster than the HBM peak, and the sweep's share of it below 1.1
+    rw = c["read_wall"]
+    assert 0 < rw["value"] < 8000.0 and 0 < rw["largest_launch"]["value"] < 8000.0
+    assert 0 < rw["sweep_fraction_of_read_wall"] < 1.1
     r = out["roofline"]
     assert r["bound"] == "hbm" and r["unit"] == "GB/s" and r["peak"] == 8000.0
     assert abs(r["frac"] - r["achieved"] / r["peak"]) < 1e-3
