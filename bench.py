@@ -29,7 +29,8 @@ For gulp at M = 3..4 the sweep is also timed with its verify rows on the
 matrix cores (radix_ops.set_policy("matrix"), config.matrix_cores). The
 ceiling beside it (config.read_wall): the same launches as plain
 non-temporal reads of their bytes (dmx_read_probe), in a graph timed the
-same way, and the largest launch's bytes read alone.
+same way, the largest launch's bytes read alone, and per launch kind (each
+kind's launches in a graph of their own) the kernel against the read.
 Reported:
   value       whole-sweep compressed-HBM GB/s = sum of algorithmic bytes /
               step time, B = 4 NW + 4 (R NB + 1) + P + 2 M C + 2 M R per
@@ -424,10 +425,36 @@ def main() -> int:
                  "largest_launch": {"bytes": big.numel() * 4, "value": round(big_gbps, 1)},
                  "kernel": f"dmx_read_probe: non-temporal 16-byte reads, {wgs} workgroups of 1024 threads, one launch "
                            "per launch of the sweep over its algorithmic bytes"}
+    # per launch kind (the launches of one shape: a layer's q/k/v, o,
+    # gate/up, down; lm_head), each kind's launches as a graph of their own:
+    # the kernel against the plain read of the same buffers' bytes
+    kinds = {}
+    for gi, sg in enumerate(sig):
+        kinds.setdefault(sg, []).append(gi)
+    per_kind = {}
+    for sg, gis in kinds.items():
+        name = "+".join(n for n, _, _ in sg)
+
+        def kernel_kind(gis=gis):
+            for gi in gis:
+                launch_group(gi)
+
+        def read_kind(gis=gis):
+            for gi in gis:
+                read_launch(rbufs[gi])
+
+        k_us = time_graph(kernel_kind, args.steps, args.warmup) * 1e3 / len(gis)
+        r_us = time_graph(read_kind, args.steps, args.warmup) * 1e3 / len(gis)
+        per_kind[name] = {"launches": len(gis), "bytes": round(sum(gbytes[gi] for gi in gis) / len(gis)),
+                          "kernel_us": round(k_us, 2), "read_us": round(r_us, 2), "kernel_over_read": round(k_us / r_us, 3)}
+    read_wall["per_launch_kind"] = per_kind
     del rbufs, big
     log(f"plain read of the same launches: {ms_r * 1e3:.1f} us, {read_wall['value']:.0f} GB/s "
         f"({read_wall['pct_of_hbm_peak']:.1f}% of peak); the sweep runs at {read_wall['sweep_fraction_of_read_wall']:.1%} "
         f"of it; the largest launch's bytes alone read at {big_gbps:.0f} GB/s")
+    for name, pk in per_kind.items():
+        log(f"  {name}: {pk['bytes'] / 1e6:.1f} MB, kernel {pk['kernel_us']:.2f} us, plain read {pk['read_us']:.2f} us "
+            f"({pk['kernel_over_read']:.2f}x), {pk['launches']} launch(es) in its graph")
     # gulp's 3- and 4-row verify: AUTO runs it on v_dot2 (measured faster);
     # the matrix policy runs it in quad units on the matrix cores, as 8 rows
     # run: the same sweep timed on that path too

@@ -76,6 +76,10 @@ def test_the_json_line_carries_the_contract():
     rw = c["read_wall"]
     assert 0 < rw["value"] < 8000.0 and 0 < rw["largest_launch"]["value"] < 8000.0
     assert 0 < rw["sweep_fraction_of_read_wall"] < 1.1
+    assert rw["per_launch_kind"], "every launch kind timed against its plain read"
+    for name, pk in rw["per_launch_kind"].items():
+        assert pk["launches"] >= 1 and pk["kernel_us"] > 0 and pk["read_us"] > 0, name
+        assert abs(pk["kernel_over_read"] - pk["kernel_us"] / pk["read_us"]) < 0.01, name
     r = out["roofline"]
     assert r["bound"] == "hbm" and r["unit"] == "GB/s" and r["peak"] == 8000.0
     assert abs(r["frac"] - r["achieved"] / r["peak"]) < 1e-3
